@@ -1,0 +1,81 @@
+#pragma once
+/// Paged KV-cache operators for the MI355X build -- the reference's operator
+/// API (include/lightllm/kv_cache/paged_attention.h:31-145 of
+/// wjb554/lightllm) with identical signatures, so EngineServer::step and the
+/// reference's tests call them unchanged.  Implemented over the C ABI in
+/// lightllm_kv.h (gfx950 HIP kernels).
+///
+/// Conventions kept from the reference:
+///  * attention returns a new Tensor of q's dtype; q's dtype must equal the
+///    pool dtype (checked here; the reference left it undefined);
+///  * block_table / seq_lens / seq_len_ptr are caller-owned device int32;
+///  * scale = 1/sqrt(head_dim) for decode and paged prefill;
+///  * head_dim > 256 throws std::runtime_error;
+///  * the decode and prefill dispatchers read the lengths back to the host
+///    (as the reference does, :555-560, :1036-1037) to size the launch; the
+///    C ABI takes host-side bounds instead and never synchronises.
+/// Extensions (new, additive): append_kv_slots (slot-mapping append),
+/// paged_prefill_varlen (N sequences in one launch), gather_kv.
+
+#include <cstdint>
+
+#include "lightllm/tensor.h"
+
+namespace lightllm {
+namespace kv_cache {
+
+class BlockAllocator;
+
+Tensor paged_attention(const Tensor& q, const int* block_table, int max_blocks_per_seq,
+                       const int* seq_lens, BlockAllocator& allocator);
+
+Tensor prefill_paged_attention(const Tensor& q, const int* block_table, int max_blocks,
+                               const int* seq_len_ptr, BlockAllocator& allocator,
+                               bool causal = false);
+
+void scatter_prefill_kv_gpu(const Tensor& k_contig, const Tensor& v_contig, int start_pos,
+                            int n_tokens, const int* block_table, int max_blocks,
+                            BlockAllocator& allocator);
+
+void scatter_prefill_kv_batched_gpu(const float* k_flat_ptr, const float* v_flat_ptr, int Hkv,
+                                    int D, const int* kv_offsets, const int* num_tokens,
+                                    const int* start_poss, const int* token_cumsum,
+                                    const int* flat_bt, int max_blocks, int N, int P_total,
+                                    BlockAllocator& allocator);
+
+void scatter_prefill_kv_batched_gpu_dispatch(DType dtype, const void* k_flat_ptr,
+                                             const void* v_flat_ptr, int Hkv, int D,
+                                             const int* kv_offsets, const int* num_tokens,
+                                             const int* start_poss, const int* token_cumsum,
+                                             const int* flat_bt, int max_blocks, int N,
+                                             int P_total, BlockAllocator& allocator);
+
+void first_prefill_attn_batched_gpu(float* out_ptr, const float* q_ptr, const float* k_ptr,
+                                    const float* v_ptr, int Hq, int Hkv, int D,
+                                    const int* offsets, const int* kv_offsets,
+                                    const int* num_tokens, const int* token_cumsum,
+                                    const int* start_poss, int N, int P_total, float scale);
+
+void first_prefill_attn_batched_gpu_dispatch(DType dtype, void* out_ptr, const void* q_ptr,
+                                             const void* k_ptr, const void* v_ptr, int Hq,
+                                             int Hkv, int D, const int* offsets,
+                                             const int* kv_offsets, const int* num_tokens,
+                                             const int* token_cumsum, const int* start_poss,
+                                             int N, int P_total, float scale);
+
+// ---- additive extensions -------------------------------------------------
+
+/// KV append by slot mapping: row i of k/v ([n, Hkv, D], pool dtype) goes to
+/// pool row slot_mapping[i] (device int64; negative = skip).
+void append_kv_slots(const Tensor& k, const Tensor& v, const int64_t* slot_mapping,
+                     BlockAllocator& allocator);
+
+/// Varlen paged prefill: q [total_q, Hq, D]; cu_q device int32 [N+1];
+/// seq_lens device int32 [N]; block_table [N, max_blocks].  Host bounds
+/// max_q_len / max_seq_len size the launch (no device read-back).
+Tensor paged_prefill_varlen(const Tensor& q, const int* block_table, int max_blocks,
+                            const int* cu_q, const int* seq_lens, int num_seqs, int max_q_len,
+                            int max_seq_len, BlockAllocator& allocator, bool causal);
+
+}  // namespace kv_cache
+}  // namespace lightllm

@@ -1,0 +1,218 @@
+/*
+ * lightllm_kv.h -- C ABI of the MI355X (gfx950) paged KV-cache hot path.
+ *
+ * Plain pointers and sizes only.  Device pointers are HIP device memory
+ * (hipMalloc / torch on ROCm); `stream` is a hipStream_t passed as void*
+ * (NULL = the null stream).  Every entry point returns 0 on success or a
+ * non-zero llkv_status; llkv_last_error() gives a message for the calling
+ * thread.  Entry points enqueue work on `stream` and do not synchronise,
+ * except where noted.
+ *
+ * Pool layout (src/kv_cache/block_allocator.cpp:24-27 of the reference):
+ *     K, V : [num_blocks, block_size, num_kv_heads, head_dim], row-major
+ * A "slot" is the row index phys * block_size + pos % block_size, with
+ * phys = block_table[pos / block_size].  Row offsets are 64-bit.
+ *
+ * Each function names the reference interface it replaces
+ * (reference = wjb554/lightllm, paths relative to its root).
+ */
+#ifndef LIGHTLLM_KV_H
+#define LIGHTLLM_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types; values equal lightllm::DType (include/lightllm/tensor.h:14). */
+enum llkv_dtype {
+    LLKV_DTYPE_F32 = 0,
+    LLKV_DTYPE_F16 = 1,
+    LLKV_DTYPE_BF16 = 2,
+    LLKV_DTYPE_I32 = 3
+};
+
+enum llkv_status {
+    LLKV_OK = 0,
+    LLKV_ERR_INVALID = 1,     /* bad argument (shape, dtype, null pointer)  */
+    LLKV_ERR_UNSUPPORTED = 2, /* e.g. head_dim > 256, as the reference      */
+    LLKV_ERR_WORKSPACE = 3,   /* workspace too small                        */
+    LLKV_ERR_HIP = 4,         /* a HIP runtime call or launch failed         */
+    LLKV_ERR_EXHAUSTED = 5    /* block pool exhausted                        */
+};
+
+const char* llkv_last_error(void);
+const char* llkv_status_string(int status);
+/* ABI version: bumped on any signature change. */
+int llkv_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * KV append by slot mapping.
+ * Replaces EngineServer::write_decode_kv (src/engine/engine_server.cpp:760-787,
+ * two cudaMemcpy per token per layer) and InferenceEngine::write_decode_kv
+ * (src/engine/engine_paged.cpp:287-331).  Row i of k_src/v_src ([n_tokens,
+ * Hkv, D], contiguous) is copied bit-exactly to pool row slot_mapping[i];
+ * a negative slot is skipped.
+ * ------------------------------------------------------------------------ */
+int llkv_append(void* k_pool, void* v_pool, const void* k_src,
+                const void* v_src, const int64_t* slot_mapping,
+                int64_t n_tokens, int num_kv_heads, int head_dim, int dtype,
+                void* stream);
+
+/* Replaces scatter_prefill_kv_gpu (include/lightllm/kv_cache/paged_attention.h:95-102,
+ * src/kv_cache/paged_attention.cu:1097-1124): token t of a chunk goes to
+ * position start_pos + t of the sequence whose table is block_table. */
+int llkv_scatter_prefill(void* k_pool, void* v_pool, const void* k_src,
+                         const void* v_src, int start_pos, int n_tokens,
+                         const int* block_table, int max_blocks,
+                         int num_kv_heads, int head_dim, int block_size,
+                         int dtype, void* stream);
+
+/* Replaces scatter_prefill_kv_batched_gpu[_dispatch]
+ * (include/lightllm/kv_cache/paged_attention.h:109-124,
+ * src/kv_cache/paged_attention.cu:1134-1219).  num_tokens is accepted for
+ * signature parity; token_cumsum[N+1] defines the entries.  All index arrays
+ * are device int32.  Unlike the reference this does not synchronise. */
+int llkv_scatter_prefill_batched(void* k_pool, void* v_pool,
+                                 const void* k_flat, const void* v_flat,
+                                 int num_kv_heads, int head_dim,
+                                 const int* kv_offsets, const int* num_tokens,
+                                 const int* start_poss,
+                                 const int* token_cumsum, const int* flat_bt,
+                                 int max_blocks, int N, int P_total,
+                                 int block_size, int dtype, void* stream);
+
+/* Block-table gather: the device form of reconstruct_kv
+ * (tests/test_paged_attention_v2.cu:219-239) and of the tile gather inside
+ * every reference kernel (load_tile_float4, src/kv_cache/paged_attention.cu:46-98).
+ * Sequence b's positions [0, cu_seqlens[b+1]-cu_seqlens[b]) are written to
+ * rows cu_seqlens[b].. of k_dst/v_dst ([total_tokens, Hkv, D]).
+ * cu_seqlens is device int32 [B+1]; block_table is [B, max_blocks]. */
+int llkv_gather(void* k_dst, void* v_dst, const void* k_pool,
+                const void* v_pool, const int* block_table, int max_blocks,
+                const int* cu_seqlens, int num_seqs, int64_t total_tokens,
+                int num_kv_heads, int head_dim, int block_size, int dtype,
+                void* stream);
+
+/* ------------------------------------------------------------------------
+ * Paged decode attention (one new token per sequence), with Split-K.
+ * Replaces lightllm::kv_cache::paged_attention
+ * (include/lightllm/kv_cache/paged_attention.h:31-36,
+ * src/kv_cache/paged_attention.cu:537-626) and its kernels (:104-532).
+ *
+ * q, out     : [num_seqs, num_q_heads, head_dim], element type `dtype`
+ *              (the pool's type, as the reference requires).
+ * block_table: device int32 [num_seqs, max_blocks_per_seq]
+ * seq_lens   : device int32 [num_seqs]; sequence b attends positions [0, len).
+ * max_seq_len: host-side upper bound of every seq_lens[b] (sizes the grid
+ *              without the reference's device-to-host read).
+ * num_splits : 0 = automatic split of each sequence's KV range;
+ *              S > 0 = the reference's fixed split (S ranges of ceil(n/S) pages).
+ * scale      : softmax scale (the reference uses 1/sqrt(head_dim)).
+ * workspace  : device memory of at least llkv_paged_decode_workspace_size()
+ *              bytes (may be NULL when that size is 0).  It must be
+ *              zero-filled before its first use; every completed call leaves
+ *              its split counters at zero again, so it can be reused without
+ *              clearing.  Calls sharing one workspace must not overlap.
+ * ------------------------------------------------------------------------ */
+size_t llkv_paged_decode_workspace_size(int num_seqs, int num_q_heads,
+                                        int num_kv_heads, int head_dim,
+                                        int block_size, int max_seq_len,
+                                        int num_splits);
+int llkv_paged_decode(void* out, const void* q, const void* k_pool,
+                      const void* v_pool, const int* block_table,
+                      const int* seq_lens, int num_seqs, int num_q_heads,
+                      int num_kv_heads, int head_dim, int block_size,
+                      int max_blocks_per_seq, int max_seq_len, int num_splits,
+                      float scale, int dtype, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Paged prefill attention over cached prefixes, varlen over N sequences.
+ * Generalises lightllm::kv_cache::prefill_paged_attention
+ * (include/lightllm/kv_cache/paged_attention.h:71-77,
+ * src/kv_cache/paged_attention.cu:1018-1092, kernels :641-974) from one
+ * sequence to N in one launch.
+ *
+ * q, out    : [total_q, num_q_heads, head_dim]; sequence n owns query rows
+ *             [cu_q[n], cu_q[n+1]) (device int32 [N+1]).
+ * seq_lens  : device int32 [N]: total keys of sequence n (history + chunk);
+ *             its chunk's K/V must already be in the pool.
+ * causal    : query row i of a chunk of P rows sits at seq_len - P + i and
+ *             attends keys at positions <= its own (self included), as the
+ *             reference kernel (src/kv_cache/paged_attention.cu:658,712).
+ * max_q_len, max_seq_len: host-side upper bounds (grid sizing).
+ * ------------------------------------------------------------------------ */
+int llkv_paged_prefill(void* out, const void* q, const void* k_pool,
+                       const void* v_pool, const int* block_table,
+                       int max_blocks_per_seq, const int* cu_q,
+                       const int* seq_lens, int num_seqs, int total_q,
+                       int max_q_len, int max_seq_len, int num_q_heads,
+                       int num_kv_heads, int head_dim, int block_size,
+                       int causal, float scale, int dtype, void* stream);
+
+/* Replaces first_prefill_attn_batched_gpu[_dispatch]
+ * (include/lightllm/kv_cache/paged_attention.h:130-145,
+ * src/kv_cache/paged_attention.cu:1230-1383): causal attention of first
+ * prefill chunks over contiguous (un-paged) K/V.  Offsets are element
+ * offsets, as in the reference.  max_tokens is a host upper bound of
+ * num_tokens[e].  Unlike the reference this does not synchronise. */
+int llkv_first_prefill_batched(void* out, const void* q, const void* k,
+                               const void* v, int num_q_heads,
+                               int num_kv_heads, int head_dim,
+                               const int* offsets, const int* kv_offsets,
+                               const int* num_tokens,
+                               const int* token_cumsum, const int* start_poss,
+                               int N, int P_total, int max_tokens, float scale,
+                               int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Host-side block pool + prefix cache (BlockAllocator, BlockTable,
+ * PrefixCache of include/lightllm/kv_cache/block_allocator.h:37-186 and
+ * prefix_cache.h:56-325), exposed as an opaque handle for non-C++ callers.
+ * policy: 0 = Hash, 1 = Radix (PrefixCachePolicy).
+ * storage: 0 = device pools (hipMalloc), 1 = host pools (malloc), 2 = no
+ * pools (metadata only; k/v pointers are NULL).
+ * ------------------------------------------------------------------------ */
+typedef struct llkv_allocator llkv_allocator;
+
+int llkv_allocator_create(int num_blocks, int block_size, int num_kv_heads,
+                          int head_dim, int policy, int dtype, int storage,
+                          llkv_allocator** out);
+void llkv_allocator_destroy(llkv_allocator* a);
+int llkv_allocator_allocate(llkv_allocator* a, uint64_t token_hash);
+int llkv_allocator_allocate_tokens(llkv_allocator* a, const int* tokens,
+                                   int n_tokens, int start_pos,
+                                   int* out_blocks, int out_capacity,
+                                   int* out_count);
+void llkv_allocator_release(llkv_allocator* a, int block_id);
+int llkv_allocator_find_by_hash(llkv_allocator* a, uint64_t token_hash);
+/* Longest cached prefix of tokens[start_pos..]: returns matched tokens,
+ * writes up to `capacity` block ids and their count. */
+int llkv_allocator_find_cached_prefix(llkv_allocator* a, const int* tokens,
+                                      int n_tokens, int start_pos,
+                                      int* block_ids, int capacity,
+                                      int* n_ids);
+void llkv_allocator_insert_cached_blocks(llkv_allocator* a, const int* tokens,
+                                         int n_tokens, int start_pos,
+                                         const int* block_ids, int n_ids);
+int llkv_allocator_evict_lru(llkv_allocator* a);
+void llkv_allocator_increment_ref(llkv_allocator* a, int block_id);
+int llkv_allocator_reset(llkv_allocator* a);
+int llkv_allocator_num_free(const llkv_allocator* a);
+int llkv_allocator_num_blocks(const llkv_allocator* a);
+int llkv_allocator_ref_count(const llkv_allocator* a, int block_id);
+uint64_t llkv_allocator_token_hash(const llkv_allocator* a, int block_id);
+size_t llkv_allocator_prefix_cache_size(const llkv_allocator* a);
+void* llkv_allocator_k_storage(llkv_allocator* a);
+void* llkv_allocator_v_storage(llkv_allocator* a);
+size_t llkv_allocator_storage_bytes(const llkv_allocator* a);
+/* FNV-1a 64 of a token block (HashPrefixCache::hash_tokens). */
+uint64_t llkv_hash_tokens(const int* tokens, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LIGHTLLM_KV_H */

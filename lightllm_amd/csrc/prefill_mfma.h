@@ -1,0 +1,44 @@
+// MFMA paged prefill attention for gfx950 (fp16 / bf16, head_dim 64 / 128,
+// 16-token pages).  Replaces the reference's scalar prefill kernels
+// (src/kv_cache/paged_attention.cu:641-974) for these shapes.
+//
+// Work-group: 4 waves, 128 query rows of one q_head (32 per wave), keys in
+// tiles of 64 (four pages) staged through LDS with double buffering.
+//
+// Per wave and key tile, with v_mfma_f32_16x16x32_{f16,bf16}:
+//   S^T = K Q^T   A = K rows from LDS (16 keys x 32 dims per MFMA),
+//                 B = Q^T held in registers for the whole kernel.
+//                 Accumulator lane l holds 4 keys of query (l % 16).
+//   online softmax per query column (row max over the lane's keys, then two
+//                 cross-lane xor steps); the lane's own keys are exactly the
+//                 k-slice it must feed to the second MFMA, so P never leaves
+//                 registers.  The key order of the A rows is permuted so that
+//                 each lane's 8 keys of a 32-key k-step are contiguous.
+//   O^T = V^T P^T A = V^T from LDS (V is transposed while staging),
+//                 B = P^T from registers.
+// Causal masking uses the reference's rule: query i of a P-row chunk over L
+// keys sits at L - P + i and sees keys <= that position.
+#pragma once
+
+#include "attn_common.h"
+
+namespace llkv {
+
+struct MfmaPrefillArgs {
+    void* out;
+    const void* q;
+    const void* k;
+    const void* v;
+    const int* bt;
+    const int* cu_q;
+    const int* lens;
+    int max_blocks, N, Hq, Hkv, causal;
+    float scale_log2;
+    int qblocks;   // query blocks per sequence (grid.x = N * qblocks)
+};
+
+// Returns -1 when the shape is not handled (caller falls back), else a status.
+int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dtype,
+                        int total_q, int max_q_len, int max_seq_len, hipStream_t st);
+
+}  // namespace llkv

@@ -1,0 +1,391 @@
+"""Parity of the gfx950 kernels (through the C ABI) against the CPU oracle.
+
+Bars:
+  * append / scatter / gather: bit-exact (compared as raw bits);
+  * fp32 attention: |gpu - ref| <= 1e-6 + 1e-5 |ref|, ref = the oracle carried in
+    double (the fp32 oracle's own rounding is of the same order, so the double
+    result is the judge, as the survey's oracle plan states);
+  * fp16 KV: |gpu - ref| <= 2e-3 (|ref| + rms(ref)), ref = double-precision oracle
+    on the fp16 values (rms(ref) is the output's RMS: an absolute floor of the
+    relative bar for outputs near zero);
+  * bf16 (not a north_star config): same form with 1.6e-2, i.e. 2 bf16 ulps.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from lightllm_amd import kv_cache as kc
+from lightllm_amd._lib import check, lib
+from lightllm_amd.kv_cache import _ptr, _stream, dtype_code
+from lightllm_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def f64(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def check_fp32(got: torch.Tensor, ref: np.ndarray, what: str, rtol=1e-5, atol=1e-6):
+    g = f64(got)
+    err = np.abs(g - ref)
+    bound = atol + rtol * np.abs(ref)
+    worst = float(err.max()) if err.size else 0.0
+    say(f"  {what}: max abs err {worst:.3e}, worst err/bound {float((err / bound).max()) if err.size else 0:.3f}")
+    assert np.all(err <= bound), f"{what}: {int((err > bound).sum())} elements out of tolerance"
+
+
+def check_lowp(got: torch.Tensor, ref: np.ndarray, what: str, rtol: float):
+    g = f64(got)
+    err = np.abs(g - ref)
+    rms = math.sqrt(float(np.mean(ref ** 2))) if ref.size else 0.0
+    bound = rtol * (np.abs(ref) + rms)
+    say(f"  {what}: max abs err {float(err.max()):.3e}, rms(ref) {rms:.3e}, "
+        f"worst err/bound {float((err / bound).max()):.3f}")
+    assert np.all(err <= bound), f"{what}: {int((err > bound).sum())} elements out of tolerance"
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16).numpy()
+    return t.view(torch.int32).numpy()
+
+
+def np_pool(t: torch.Tensor) -> np.ndarray:
+    """Host copy of a pool as float32 (exact widening of fp16/bf16)."""
+    return t.detach().float().cpu().numpy()
+
+
+# ---------------------------------------------------------------------------
+# copies
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_append_bit_exact(dtype):
+    say(f"append dtype={dtype}")
+    g = torch.Generator().manual_seed(10)
+    nb, hkv, d = 64, 2, 64
+    kp = torch.randn(nb, 16, hkv, d, generator=g).to(dtype)
+    vp = torch.randn(nb, 16, hkv, d, generator=g).to(dtype)
+    n = 200
+    slots = torch.randperm(nb * 16, generator=g)[:n].to(torch.int64)
+    slots[::17] = -1   # skipped rows
+    kn = torch.randn(n, hkv, d, generator=g).to(dtype)
+    vn = torch.randn(n, hkv, d, generator=g).to(dtype)
+    kd, vd = kp.to(DEV), vp.to(DEV)
+    kc.append_kv(kn.to(DEV), vn.to(DEV), slots.to(DEV), kd, vd)
+    torch.cuda.synchronize()
+    ke, ve = bits(kp).copy(), bits(vp).copy()
+    oracle.append_slots(ke, ve, bits(kn), bits(vn), slots.numpy())
+    assert np.array_equal(bits(kd), ke) and np.array_equal(bits(vd), ve)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_scatter_and_gather_round_trip(dtype):
+    say(f"scatter/gather dtype={dtype}")
+    g = torch.Generator().manual_seed(11)
+    nb, hkv, d = 128, 2, 64
+    lens = [1, 16, 17, 100, 333]
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    mb = max((L + 15) // 16 for L in lens)
+    table, _ = wl._tables(lens, perm, mb)
+    kp = torch.zeros(nb, 16, hkv, d, dtype=dtype, device=DEV)
+    vp = torch.zeros_like(kp)
+    srcs = []
+    for i, L in enumerate(lens):
+        k = torch.randn(L, hkv, d, generator=g).to(dtype)
+        v = torch.randn(L, hkv, d, generator=g).to(dtype)
+        srcs.append((k, v))
+        # positions [0, L) written as two chunks to exercise start_pos
+        h = L // 2
+        row = table[i].to(DEV)
+        for s, e in ((0, h), (h, L)):
+            if e > s:
+                kk, vv = k[s:e].to(DEV), v[s:e].to(DEV)
+                check(lib().llkv_scatter_prefill(_ptr(kp), _ptr(vp), _ptr(kk), _ptr(vv), s, e - s,
+                                                 _ptr(row), mb, hkv, d, 16, dtype_code(dtype),
+                                                 _stream()))
+        torch.cuda.synchronize()
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    kg, vg = kc.gather_kv(kp, vp, table.to(DEV), cu.to(DEV), int(cu[-1]))
+    torch.cuda.synchronize()
+    # round trip: gather(scatter(x)) == x bit-exactly
+    assert np.array_equal(bits(kg), bits(torch.cat([s[0] for s in srcs])))
+    assert np.array_equal(bits(vg), bits(torch.cat([s[1] for s in srcs])))
+    # and the gather equals the oracle's reconstruct_kv of the same pool
+    kh, vh = bits(kp), bits(vp)
+    for i, L in enumerate(lens):
+        ko, vo = oracle.reconstruct_kv(kh, vh, table[i].numpy(), L)
+        assert np.array_equal(bits(kg)[cu[i]:cu[i + 1]], ko)
+        assert np.array_equal(bits(vg)[cu[i]:cu[i + 1]], vo)
+
+
+def test_scatter_batched_bit_exact():
+    say("scatter batched fp16")
+    g = torch.Generator().manual_seed(12)
+    nb, hkv, d, dtype = 128, 2, 64, torch.float16
+    ntok = [5, 40, 16, 70]
+    starts = [0, 0, 32, 3]
+    n = len(ntok)
+    cum = np.concatenate([[0], np.cumsum(ntok)]).astype(np.int32)
+    kv_off = (cum[:-1] * hkv * d).astype(np.int32)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    mb = 8
+    flat = torch.full((n, mb), -1, dtype=torch.int32)
+    pos = 0
+    for e in range(n):
+        need = (starts[e] + ntok[e] + 15) // 16
+        flat[e, :need] = perm[pos:pos + need]
+        pos += need
+    alloc = kc.BlockAllocator(nb, 16, hkv, d, kv_dtype=dtype, device=DEV)
+    kf = torch.randn(int(cum[-1]), hkv, d, generator=g).to(dtype)
+    vf = torch.randn(int(cum[-1]), hkv, d, generator=g).to(dtype)
+    t32 = lambda a: torch.as_tensor(np.asarray(a), dtype=torch.int32).to(DEV)
+    kc.scatter_prefill_kv_batched(kf.to(DEV), vf.to(DEV), t32(kv_off), t32(ntok), t32(starts),
+                                  t32(cum), flat.to(DEV).contiguous(), mb, n, int(cum[-1]), alloc)
+    torch.cuda.synchronize()
+    ke = np.zeros_like(bits(alloc.k_storage))
+    ve = np.zeros_like(ke)
+    oracle.scatter_prefill_batched(ke, ve, bits(kf), bits(vf), kv_off, starts, cum, flat.numpy(), mb)
+    assert np.array_equal(bits(alloc.k_storage), ke) and np.array_equal(bits(alloc.v_storage), ve)
+
+
+# ---------------------------------------------------------------------------
+# decode
+# ---------------------------------------------------------------------------
+
+def run_decode(case: wl.DecodeCase, num_splits=0, append=True):
+    kp, vp = case.k_pool.to(DEV), case.v_pool.to(DEV)
+    if append and case.k_new is not None:
+        kc.append_kv(case.k_new.to(DEV), case.v_new.to(DEV), case.slots.to(DEV), kp, vp)
+    out = kc.paged_decode(case.q.to(DEV), kp, vp, case.block_table.to(DEV), case.seq_lens.to(DEV),
+                          case.max_seq_len, num_splits=num_splits, scale=case.scale)
+    torch.cuda.synchronize()
+    return out, kp, vp
+
+
+def oracle_decode(case: wl.DecodeCase, kp: np.ndarray, vp: np.ndarray, threads=8):
+    return oracle.paged_decode(case.q.float().numpy(), kp, vp, case.block_table.numpy(),
+                               case.seq_lens.numpy(), f64=True, nthreads=threads)
+
+
+def test_decode_config1():
+    say("decode config 1: B=1 14/2/64 fp32 L=512 pool 4096")
+    case = wl.config1()
+    out, _, _ = run_decode(case)
+    ref = oracle_decode(case, case.k_pool.numpy(), case.v_pool.numpy())
+    check_fp32(out, ref, "cfg1 decode")
+    r32 = oracle.paged_decode(case.q.numpy(), case.k_pool.numpy(), case.v_pool.numpy(),
+                              case.block_table.numpy(), case.seq_lens.numpy())
+    say(f"  (fp32 oracle vs double oracle: max abs diff {np.abs(r32 - ref).max():.3e})")
+
+
+def test_decode_config2_append_then_decode():
+    say("decode config 2: B=64 fp32 append + decode, pool 32768")
+    case = wl.config2()
+    out, kp, vp = run_decode(case)
+    # append is bit-exact against the oracle's slot copy
+    ke, ve = case.k_pool.numpy().copy(), case.v_pool.numpy().copy()
+    oracle.append_slots(ke, ve, case.k_new.numpy(), case.v_new.numpy(), case.slots.numpy())
+    assert torch.equal(kp, torch.from_numpy(ke).to(DEV)) and torch.equal(vp, torch.from_numpy(ve).to(DEV))
+    ref = oracle_decode(case, ke, ve)
+    check_fp32(out, ref, "cfg2 decode (auto split)")
+    for s in (1, 4):
+        o2 = kc.paged_decode(case.q.to(DEV), kp, vp, case.block_table.to(DEV),
+                             case.seq_lens.to(DEV), case.max_seq_len, num_splits=s)
+        torch.cuda.synchronize()
+        check_fp32(o2, ref, f"cfg2 decode S={s}")
+
+
+@pytest.mark.parametrize("splits", [4, 16, 0])
+def test_decode_config3_fp16_splitk(splits):
+    say(f"decode config 3: B=16 L=32768 fp16 outliers, S={splits}")
+    case = wl.config3()
+    out, _, _ = run_decode(case, num_splits=splits, append=False)
+    ref = oracle_decode(case, np_pool(case.k_pool), np_pool(case.v_pool), threads=16)
+    check_lowp(out, ref, f"cfg3 decode S={splits}", 2e-3)
+
+
+EDGE = [
+    # (name, Hq, Hkv, D, lengths, dtype)
+    ("seq1", 14, 2, 64, [1], torch.float32),
+    ("seq_sweep", 14, 2, 64, [8, 15, 16, 17, 31, 33, 64, 100, 255, 256, 257, 512, 1000, 1024],
+     torch.float32),
+    ("D63", 4, 2, 63, [40, 100], torch.float32),
+    ("D65", 4, 2, 65, [40, 100], torch.float32),
+    ("D67", 4, 2, 67, [40, 100], torch.float32),
+    ("D32", 4, 2, 32, [40, 100], torch.float32),
+    ("D128_hq32_hkv8", 32, 8, 128, [300, 17], torch.float32),
+    ("D256", 8, 2, 256, [77, 300], torch.float32),
+    ("gqa_8_2", 8, 2, 64, [200, 33], torch.float32),
+    ("mqa_hkv1", 8, 1, 64, [200, 33], torch.float32),
+    ("mha", 4, 4, 64, [200, 33], torch.float32),
+    ("gqa_g3_generic", 6, 2, 64, [130, 5], torch.float32),
+    ("fp16_D128_g4", 32, 8, 128, [1, 500, 2049], torch.float16),
+    ("fp16_D64_g7", 14, 2, 64, [7, 700], torch.float16),
+    ("bf16_D64_g7", 14, 2, 64, [7, 700], torch.bfloat16),
+    ("bf16_D128_g4", 32, 8, 128, [3, 900], torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("name,hq,hkv,d,lengths,dtype", EDGE, ids=[e[0] for e in EDGE])
+def test_decode_edge_cases(name, hq, hkv, d, lengths, dtype):
+    say(f"decode edge {name}: Hq={hq} Hkv={hkv} D={d} L={lengths} {dtype}")
+    need = sum((L + 1 + 15) // 16 for L in lengths)
+    case = wl.decode_case(name, len(lengths), hq, hkv, d, lengths, need + 8, dtype, seed=len(name))
+    for s in (0, 4):
+        out, kp, vp = run_decode(case, num_splits=s, append=(s == 0))
+        if s == 0:
+            kh, vh = np_pool(kp), np_pool(vp)
+        ref = oracle_decode(case, kh, vh)
+        if dtype == torch.float32:
+            check_fp32(out, ref, f"{name} S={s}")
+        else:
+            check_lowp(out, ref, f"{name} S={s}", 2e-3 if dtype == torch.float16 else 1.6e-2)
+        case.k_pool, case.v_pool = kp.cpu(), vp.cpu()
+
+
+def test_decode_noncontiguous_table_and_empty():
+    say("decode: table [7,3,11], zero-length sequence in a batch")
+    g = torch.Generator().manual_seed(13)
+    hq, hkv, d = 8, 2, 64
+    kp = torch.randn(16, 16, hkv, d, generator=g)
+    vp = torch.randn(16, 16, hkv, d, generator=g)
+    table = torch.tensor([[7, 3, 11], [-1, -1, -1], [5, -1, -1]], dtype=torch.int32)
+    lens = torch.tensor([40, 0, 1], dtype=torch.int32)
+    q = torch.randn(3, hq, d, generator=g)
+    out = kc.paged_decode(q.to(DEV), kp.to(DEV), vp.to(DEV), table.to(DEV), lens.to(DEV), 40)
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(q.numpy(), kp.numpy(), vp.numpy(), table.numpy(), lens.numpy(), f64=True)
+    check_fp32(out, ref, "[7,3,11] + empty + L=1")
+    assert torch.count_nonzero(out[1]).item() == 0
+    # L=1 returns V[0] exactly up to the fp32 division by l=1
+    assert torch.allclose(out[2].cpu(), vp[5, 0].repeat_interleave(hq // hkv, 0), rtol=0, atol=1e-7)
+
+
+def test_decode_invalid_arguments():
+    from lightllm_amd import LLKVError
+    q = torch.zeros(1, 4, 320, device=DEV)
+    kp = torch.zeros(2, 16, 2, 320, device=DEV)
+    with pytest.raises(LLKVError):
+        kc.paged_decode(q, kp, kp, torch.zeros(1, 1, dtype=torch.int32, device=DEV),
+                        torch.ones(1, dtype=torch.int32, device=DEV), 1)
+
+
+# ---------------------------------------------------------------------------
+# prefill
+# ---------------------------------------------------------------------------
+
+def run_prefill(case: wl.PrefillCase, kp=None, vp=None):
+    kp = case.k_pool.to(DEV) if kp is None else kp
+    vp = case.v_pool.to(DEV) if vp is None else vp
+    kc.append_kv(case.k_chunk.to(DEV), case.v_chunk.to(DEV), case.slots.to(DEV), kp, vp)
+    out = kc.paged_prefill(case.q.to(DEV), kp, vp, case.block_table.to(DEV), case.cu_q.to(DEV),
+                           case.seq_lens.to(DEV), case.max_q_len, case.max_seq_len,
+                           causal=case.causal, scale=case.scale)
+    torch.cuda.synchronize()
+    return out, kp, vp
+
+
+def oracle_prefill(case: wl.PrefillCase, kp, vp, threads=16):
+    return oracle.paged_prefill(case.q.float().numpy(), case.cu_q.numpy(), np_pool(kp), np_pool(vp),
+                                case.block_table.numpy(), case.seq_lens.numpy(), case.causal,
+                                f64=True, nthreads=threads)
+
+
+def test_prefill_config4_fp16():
+    say("prefill config 4: 8x512 chunks, prefixes {0,256,1024,4096x3 shared,2048,512}, fp16 causal")
+    case = wl.config4()
+    out, kp, vp = run_prefill(case)
+    ref = oracle_prefill(case, kp, vp)
+    check_lowp(out, ref, "cfg4 prefill", 2e-3)
+
+
+PREFILL = [
+    # (name, Hq, Hkv, D, prefixes, chunks, dtype, causal)
+    ("fp32_small_causal", 14, 2, 64, [0, 20, 33], [7, 64, 130], torch.float32, True),
+    ("fp32_small_noncausal", 14, 2, 64, [0, 20, 33], [7, 64, 130], torch.float32, False),
+    ("fp32_P1", 4, 2, 64, [100], [1], torch.float32, True),
+    ("fp32_D67", 4, 2, 67, [10], [30], torch.float32, True),
+    ("fp16_D64_unaligned", 14, 2, 64, [5, 300, 0], [1, 129, 200], torch.float16, True),
+    ("fp16_D64_noncausal", 14, 2, 64, [48, 0], [70, 300], torch.float16, False),
+    ("fp16_D128", 32, 8, 128, [0, 1000], [256, 77], torch.float16, True),
+    ("bf16_D64", 14, 2, 64, [16, 200], [100, 256], torch.bfloat16, True),
+    ("bf16_D128", 32, 8, 128, [64], [200], torch.bfloat16, True),
+    ("fp16_mha", 4, 4, 64, [31], [97], torch.float16, True),
+]
+
+
+@pytest.mark.parametrize("name,hq,hkv,d,prefixes,chunks,dtype,causal", PREFILL,
+                         ids=[p[0] for p in PREFILL])
+def test_prefill_cases(name, hq, hkv, d, prefixes, chunks, dtype, causal):
+    say(f"prefill {name}")
+    nb = sum((p + c + 15) // 16 for p, c in zip(prefixes, chunks)) + 4
+    case = wl.prefill_case(name, hq, hkv, d, prefixes, chunks, {}, nb, dtype, seed=len(name),
+                           causal=causal)
+    out, kp, vp = run_prefill(case)
+    ref = oracle_prefill(case, kp, vp)
+    if dtype == torch.float32:
+        check_fp32(out, ref, name)
+    else:
+        check_lowp(out, ref, name, 2e-3 if dtype == torch.float16 else 1.6e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_first_prefill_batched(dtype):
+    say(f"first prefill batched {dtype}")
+    g = torch.Generator().manual_seed(14)
+    hq, hkv, d = 14, 2, 64
+    ntok = [1, 37, 128, 300]
+    n = len(ntok)
+    cum = np.concatenate([[0], np.cumsum(ntok)]).astype(np.int32)
+    offs = (cum[:-1] * hq * d).astype(np.int32)
+    kvoffs = (cum[:-1] * hkv * d).astype(np.int32)
+    starts = np.zeros(n, dtype=np.int32)
+    ptot = int(cum[-1])
+    q = torch.randn(ptot, hq, d, generator=g).to(dtype)
+    k = torch.randn(ptot, hkv, d, generator=g).to(dtype)
+    v = torch.randn(ptot, hkv, d, generator=g).to(dtype)
+    out = torch.zeros(ptot, hq, d, dtype=dtype, device=DEV)
+    t32 = lambda a: torch.as_tensor(a, dtype=torch.int32).to(DEV)
+    kc.first_prefill_attn_batched(out, q.to(DEV), k.to(DEV), v.to(DEV), hq, hkv, d, t32(offs),
+                                  t32(kvoffs), t32(ntok), t32(cum), t32(starts), n, ptot,
+                                  1.0 / math.sqrt(d))
+    torch.cuda.synchronize()
+    # reference rule: entry e is causal over its own contiguous keys
+    ref = np.zeros((ptot, hq, d))
+    for e in range(n):
+        s, t = cum[e], cum[e + 1]
+        ref[s:t] = oracle.prefill_attention(q[s:t].float().numpy(), k[s:t].float().numpy(),
+                                            v[s:t].float().numpy(), True, f64=True)
+    if dtype == torch.float32:
+        check_fp32(out, ref, "first_prefill fp32")
+        r32 = oracle.first_prefill_batched(q.numpy(), k.numpy(), v.numpy(), hq, hkv, d, offs, kvoffs,
+                                           ntok, cum, starts, 1.0 / math.sqrt(d), ptot)
+        say(f"  (restated kernel oracle vs double: {np.abs(r32 - ref).max():.3e})")
+    else:
+        check_lowp(out, ref, "first_prefill fp16", 2e-3)
+
+
+# ---------------------------------------------------------------------------
+# C++ API (reference signatures) on the GPU
+# ---------------------------------------------------------------------------
+
+def test_cxx_api_gpu():
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(__file__), "cpp", "_bin", "test_cxx_api")
+    assert os.path.exists(exe), "build tests/cpp first (__graft_entry__.build())"
+    say("C++ API test binary (gpu)")
+    r = subprocess.run([exe, "gpu"], capture_output=True, text=True, timeout=120)
+    say(r.stdout + r.stderr)
+    assert r.returncode == 0
