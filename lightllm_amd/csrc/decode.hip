@@ -106,7 +106,7 @@ __global__ __launch_bounds__(64) void decode_fast_kernel(DecodeArgs a) {
         for (int u = 0; u < U; ++u) {
             const int ts = t0 + u * TPS;                  // first token of the step (uniform)
             const int page = min(ts >> 4, last_page);     // steps past the end re-read a valid page
-            const int64_t phys = bt[page];
+            const int64_t phys = max(bt[page], 0);          // a -1 hole reads page 0, never faults
             const int64_t row = phys * kPage + (ts & 15) + grp;
             const T* kp = kbase + row * row_elems;
             const T* vp = vbase + row * row_elems;
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeArgs a) {
         int64_t row = 0;
         float s = -INFINITY;
         if (valid) {
-            row = ((int64_t)bt[t / a.bs] * a.bs + t % a.bs) * row_elems + (int64_t)kvh * D;
+            row = ((int64_t)max(bt[t / a.bs], 0) * a.bs + t % a.bs) * row_elems + (int64_t)kvh * D;
             float d0 = 0.0f;
             for (int d = 0; d < D; ++d) d0 = fmaf(q_s[d], Elem<T>::to_f32(kp[row + d]), d0);
             s = d0;

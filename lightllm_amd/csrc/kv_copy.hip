@@ -60,6 +60,7 @@ struct BatchedMap {  // scatter_prefill_batched
         int e = find_entry(token_cumsum, N, (int)g);
         int local = (int)g - token_cumsum[e];
         int pos = start_poss[e] + local;
+        if (pos < 0 || pos / block_size >= max_blocks) return false;   // outside the table
         int64_t phys = flat_bt[(int64_t)e * max_blocks + pos / block_size];
         s = (int64_t)kv_offsets[e] * esize + (int64_t)local * row_bytes;
         d = (phys * block_size + pos % block_size) * row_bytes;
@@ -75,6 +76,7 @@ struct GatherMap {  // gather: output row g -> pool row of its (seq, pos)
     __device__ bool operator()(int64_t g, int64_t& s, int64_t& d) const {
         int b = find_entry(cu_seqlens, B, (int)g);
         int pos = (int)g - cu_seqlens[b];
+        if (pos < 0 || pos / block_size >= max_blocks) return false;   // outside the table
         int64_t phys = table[(int64_t)b * max_blocks + pos / block_size];
         s = (phys * block_size + pos % block_size) * row_bytes;
         d = g * row_bytes;

@@ -106,7 +106,7 @@ __global__ __launch_bounds__(64) void rows_generic_kernel(RowArgs a) {
         float s = -INFINITY;
         if (valid) {
             if (PAGED)
-                row = ((int64_t)bt[t / a.bs] * a.bs + t % a.bs) * row_elems + (int64_t)kvh * D;
+                row = ((int64_t)max(bt[t / a.bs], 0) * a.bs + t % a.bs) * row_elems + (int64_t)kvh * D;
             else
                 row = kv_base + (int64_t)t * row_elems + (int64_t)kvh * D;
             float d0 = 0.0f;

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             const int ch = tid + 256 * j;
             const int key = ch / (D / 8), c = ch % (D / 8);
             const int page = min((key0 + key) >> 4, last_page);
-            const int64_t row = (int64_t)bt[page] * kPage + ((key0 + key) & 15);
+            const int64_t row = (int64_t)max(bt[page], 0) * kPage + ((key0 + key) & 15);
             kreg[j] = *reinterpret_cast<const uint4*>(kg + row * row_elems + c * 8);
         }
 #pragma unroll
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             const int kp = task % (BN / 2), c = task / (BN / 2);
             const int key = key0 + 2 * kp;
             const int page = min(key >> 4, last_page);
-            const int64_t row = (int64_t)bt[page] * kPage + (key & 15);
+            const int64_t row = (int64_t)max(bt[page], 0) * kPage + (key & 15);
             vreg[j][0] = *reinterpret_cast<const uint4*>(vg + row * row_elems + c * 8);
             vreg[j][1] = *reinterpret_cast<const uint4*>(vg + (row + 1) * row_elems + c * 8);
         }
