@@ -116,6 +116,8 @@ int llkv_gather(void* k_dst, void* v_dst, const void* k_pool,
  *              zero-filled before its first use; every completed call leaves
  *              its split counters at zero again, so it can be reused without
  *              clearing.  Calls sharing one workspace must not overlap.
+ *              Its first 256 KiB hold the split counters (one per sequence x
+ *              q head), so num_seqs * num_q_heads <= 65536 when splitting.
  * ------------------------------------------------------------------------ */
 size_t llkv_paged_decode_workspace_size(int num_seqs, int num_q_heads,
                                         int num_kv_heads, int head_dim,

@@ -356,8 +356,13 @@ Plan make_plan(int B, int Hkv, int bs, int max_seq_len, int num_splits) {
     return p;
 }
 
-// Workspace: [counters B*Hq int32, 256 B aligned][lse B*Hq*S_max][o B*Hq*S_max*D].
-size_t counter_bytes(int B, int Hq) { return ((size_t)B * Hq * sizeof(int) + 255) & ~(size_t)255; }
+// Workspace: [counters: fixed kCounterBytes][lse B*Hq*S_max][o B*Hq*S_max*D].
+// The counter region has the same size and place for every call, so a
+// workspace reused across batch shapes never finds partial data where a
+// counter is expected (the counters are zero between calls).
+constexpr size_t kCounterBytes = 256 * 1024;
+constexpr int kMaxHeadRows = (int)(kCounterBytes / sizeof(int));   // B * Hq limit
+size_t counter_bytes(int, int) { return kCounterBytes; }
 
 size_t workspace_for(int B, int Hq, int D, const Plan& p) {
     if (p.S_max <= 1) return 0;
@@ -405,6 +410,9 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
     if (max_seq_len > max_blocks_per_seq * block_size) max_seq_len = max_blocks_per_seq * block_size;
 
     Plan p = make_plan(num_seqs, num_kv_heads, block_size, max_seq_len, num_splits);
+    if (p.S_max > 1 && (int64_t)num_seqs * num_q_heads > kMaxHeadRows)
+        return set_error(LLKV_ERR_UNSUPPORTED, "%s: num_seqs * num_q_heads %lld exceeds %d", fn,
+                         (long long)num_seqs * num_q_heads, kMaxHeadRows);
     size_t need = workspace_for(num_seqs, num_q_heads, head_dim, p);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
         return set_error(LLKV_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn,

@@ -5,9 +5,10 @@ Bars:
   * fp32 attention: |gpu - ref| <= 1e-6 + 1e-5 |ref|, ref = the oracle carried in
     double (the fp32 oracle's own rounding is of the same order, so the double
     result is the judge, as the survey's oracle plan states);
-  * fp16 KV: |gpu - ref| <= 2e-3 (|ref| + rms(ref)), ref = double-precision oracle
-    on the fp16 values (rms(ref) is the output's RMS: an absolute floor of the
-    relative bar for outputs near zero);
+  * fp16 KV: |gpu - ref| <= 2e-3 (|ref| + rms_D(ref)), ref = double-precision
+    oracle on the fp16 values, rms_D = RMS of that output vector over head_dim
+    (the relative bar taken against the vector's magnitude, so components near
+    zero are not held to a bar below the fp16 rounding of the vector);
   * bf16 (not a north_star config): same form with 1.6e-2, i.e. 2 bf16 ulps.
 """
 import math
@@ -46,9 +47,10 @@ def check_fp32(got: torch.Tensor, ref: np.ndarray, what: str, rtol=1e-5, atol=1e
 def check_lowp(got: torch.Tensor, ref: np.ndarray, what: str, rtol: float):
     g = f64(got)
     err = np.abs(g - ref)
-    rms = math.sqrt(float(np.mean(ref ** 2))) if ref.size else 0.0
+    # relative to each output vector's RMS (over head_dim), plus the element itself
+    rms = np.sqrt(np.mean(ref ** 2, axis=-1, keepdims=True))
     bound = rtol * (np.abs(ref) + rms)
-    say(f"  {what}: max abs err {float(err.max()):.3e}, rms(ref) {rms:.3e}, "
+    say(f"  {what}: max abs err {float(err.max()):.3e}, "
         f"worst err/bound {float((err / bound).max()):.3f}")
     assert np.all(err <= bound), f"{what}: {int((err > bound).sum())} elements out of tolerance"
 
