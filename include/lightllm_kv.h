@@ -112,12 +112,8 @@ int llkv_gather(void* k_dst, void* v_dst, const void* k_pool,
  *              S > 0 = the reference's fixed split (S ranges of ceil(n/S) pages).
  * scale      : softmax scale (the reference uses 1/sqrt(head_dim)).
  * workspace  : device memory of at least llkv_paged_decode_workspace_size()
- *              bytes (may be NULL when that size is 0).  It must be
- *              zero-filled before its first use; every completed call leaves
- *              its split counters at zero again, so it can be reused without
- *              clearing.  Calls sharing one workspace must not overlap.
- *              Its first 256 KiB hold the split counters (one per sequence x
- *              q head), so num_seqs * num_q_heads <= 65536 when splitting.
+ *              bytes (may be NULL when that size is 0); it holds the split
+ *              partials.  Calls sharing one workspace must not overlap.
  * ------------------------------------------------------------------------ */
 size_t llkv_paged_decode_workspace_size(int num_seqs, int num_q_heads,
                                         int num_kv_heads, int head_dim,

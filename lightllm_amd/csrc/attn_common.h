@@ -8,9 +8,7 @@ namespace llkv {
 
 // Arguments of the decode kernels.  Partials: part_o [B, Hq, S_max, D] fp32
 // holding the normalised split output, part_lse [B, Hq, S_max] holding the
-// split's log2-sum-exp2 (in the base-2 domain of the scaled scores);
-// counters [B, Hq] int32 count finished splits (zero between calls: the split
-// that completes a head group merges the partials and resets its counter).
+// split's log2-sum-exp2 (in the base-2 domain of the scaled scores).
 struct DecodeArgs {
     void* out;
     const void* q;
@@ -20,7 +18,6 @@ struct DecodeArgs {
     const int* lens;
     float* part_o;
     float* part_lse;
-    int* counters;
     int B, Hq, Hkv, D, bs, max_blocks;
     int S_max;      // splits allocated per (seq, head)
     int pps_auto;   // pages per split in automatic mode
@@ -58,50 +55,11 @@ __device__ inline SplitGeo split_geo(const DecodeArgs& a, int b) {
 
 constexpr float kNegBig = -1e30f;   // finite "minus infinity" for running maxima
 
-// Split completion: called by every lane of the wave after it stored its
-// partial.  Returns true in exactly one wave per counter -- the last split to
-// finish -- after making the other splits' partials visible to it.  Release /
-// acquire are at agent scope, so partials written through another XCD's L2
-// are written back before the count and re-read from memory after it.
-__device__ inline bool split_arrive_last(int* counter, int nsplit) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    int prev = 0;
-    if (threadIdx.x == 0)
-        prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __shfl(prev, 0, 64);
-    if (prev != nsplit - 1) return false;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    return true;
-}
-
-// Merge of the nsplit partials of `heads` consecutive q heads starting at
-// (b, hq0) into `out` (the reference's paged_attention_reduce_kernel,
-// src/kv_cache/paged_attention.cu:477-532, in normalised form:
-// out = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M)).  One wave; lanes own
-// output dims.  Resets the counter for the next call.
-template <typename T>
-__device__ inline void split_merge(const DecodeArgs& a, int b, int hq0, int heads, int nsplit,
-                                   int* counter) {
-    const int lane = threadIdx.x;
-    for (int g = 0; g < heads; ++g) {
-        const int64_t bh = (int64_t)b * a.Hq + hq0 + g;
-        const float* lse = a.part_lse + bh * a.S_max;
-        const float* po = a.part_o + bh * a.S_max * a.D;
-        float M = -INFINITY;
-        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, lse[s]);
-        float wsum = 0.0f;
-        for (int s = 0; s < nsplit; ++s) wsum += fast_exp2(lse[s] - M);
-        const float inv = 1.0f / wsum;
-        T* out = reinterpret_cast<T*>(a.out) + bh * a.D;
-        for (int d = lane; d < a.D; d += 64) {
-            float o = 0.0f;
-            for (int s = 0; s < nsplit; ++s)
-                o = fmaf(fast_exp2(lse[s] - M),
-                         po[(int64_t)s * a.D + d], o);
-            out[d] = Elem<T>::from_f32(o * inv);
-        }
-    }
-    if (lane == 0) *counter = 0;
-}
+// Optional per-work-group timeline for experiments: a build may define
+// LLKV_TRACE_POINT(k) to record a timestamp at point k; by default it compiles
+// to nothing.
+#ifndef LLKV_TRACE_POINT
+#define LLKV_TRACE_POINT(k)
+#endif
 
 }  // namespace llkv

@@ -19,199 +19,20 @@
 //    of the split, where the groups are merged by log-sum-exp with shuffles.
 //  * Split-K is per sequence: a sequence of n pages gets ceil(n/pps) splits
 //    (automatic) or the reference's S ranges of ceil(n/S) pages (fixed), so
-//    short sequences in a mixed batch launch no idle split.  The split that
-//    finishes last for a (sequence, kv_head) -- detected with an agent-scope
-//    atomic counter -- merges the partials by log-sum-exp in the same launch;
-//    a sequence with one split writes the output directly.
+//    short sequences in a mixed batch launch no idle split.  Partials are
+//    merged by log-sum-exp in a small second kernel; a sequence with one
+//    split writes the output directly.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cmath>
 
 #include "attn_common.h"
+#include "decode_fast.h"
+#include "decode_mfma.h"
 
 namespace llkv {
 namespace {
-
-template <typename T, int D, int G>
-struct FastCfg {
-    static constexpr int VEC = Chunk<T>::VEC;          // elements per 16 B
-    static constexpr int NJ = sizeof(T) == 4 ? 2 : 1;   // 16 B chunks per lane
-    static constexpr int DPL = NJ * VEC;                // dims per lane (8)
-    static constexpr int LPT = D / DPL;                 // lanes per token
-    static constexpr int TPS = 64 / LPT;                // tokens per step
-    static constexpr int U = 8 / NJ;                    // steps per tile
-    static constexpr int TILE = U * TPS;
-    static_assert(D % DPL == 0, "head_dim must be a multiple of 8");
-    static_assert(TPS >= 1 && TPS <= 16 && 16 % TPS == 0, "step must stay inside a page");
-};
-
-template <typename T, int D, int G>
-__global__ __launch_bounds__(64) void decode_fast_kernel(DecodeArgs a) {
-    using C = FastCfg<T, D, G>;
-    constexpr int VEC = C::VEC, NJ = C::NJ, DPL = C::DPL, LPT = C::LPT;
-    constexpr int TPS = C::TPS, U = C::U, TILE = C::TILE;
-
-    const int lane = threadIdx.x;
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const SplitGeo geo = split_geo(a, b);
-    const int hq0 = kvh * G;
-    T* out = reinterpret_cast<T*>(a.out);
-
-    if (geo.npages == 0) {   // empty sequence: zeros, as the reference (:224-227)
-        if (split == 0) {
-            for (int i = lane; i < G * D; i += 64)
-                out[((int64_t)b * a.Hq + hq0) * D + i] = Elem<T>::from_f32(0.0f);
-        }
-        return;
-    }
-    if (split >= geo.nsplit) return;
-
-    const int tok_begin = split * geo.pps * kPage;
-    const int tok_end = min(tok_begin + geo.pps * kPage, geo.L);
-    const int last_page = (tok_end - 1) >> 4;
-    const int grp = lane / LPT, part = lane % LPT;
-
-    // Query rows of the G heads, pre-scaled into the exp2 domain.
-    float qf[G][DPL];
-    const T* qb = reinterpret_cast<const T*>(a.q) + ((int64_t)b * a.Hq + hq0) * D;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            uint4 c = *reinterpret_cast<const uint4*>(qb + g * D + (j * LPT + part) * VEC);
-            Chunk<T>::unpack(c, &qf[g][j * VEC]);
-        }
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) qf[g][e] *= a.scale_log2;
-    }
-
-    float m[G], l[G], acc[G][DPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = kNegBig;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[g][e] = 0.0f;
-    }
-
-    const int64_t row_elems = (int64_t)a.Hkv * D;
-    const T* kbase = reinterpret_cast<const T*>(a.k) + kvh * D + part * VEC;
-    const T* vbase = reinterpret_cast<const T*>(a.v) + kvh * D + part * VEC;
-    const int* bt = a.bt + (int64_t)b * a.max_blocks;
-
-    for (int t0 = tok_begin; t0 < tok_end; t0 += TILE) {
-        uint4 kr[U][NJ], vr[U][NJ];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int ts = t0 + u * TPS;                  // first token of the step (uniform)
-            const int page = min(ts >> 4, last_page);     // steps past the end re-read a valid page
-            const int64_t phys = max(bt[page], 0);          // a -1 hole reads page 0, never faults
-            const int64_t row = phys * kPage + (ts & 15) + grp;
-            const T* kp = kbase + row * row_elems;
-            const T* vp = vbase + row * row_elems;
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                kr[u][j] = *reinterpret_cast<const uint4*>(kp + j * LPT * VEC);
-                vr[u][j] = *reinterpret_cast<const uint4*>(vp + j * LPT * VEC);
-            }
-        }
-
-        float s[U][G];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float kf[DPL];
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) Chunk<T>::unpack(kr[u][j], &kf[j * VEC]);
-            const bool valid = (t0 + u * TPS + grp) < tok_end;
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float d = 0.0f;
-#pragma unroll
-                for (int e = 0; e < DPL; ++e) d = fmaf(qf[g][e], kf[e], d);
-                d = group_sum<LPT>(d);
-                s[u][g] = valid ? d : -INFINITY;
-            }
-        }
-
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float mx = m[g];
-#pragma unroll
-            for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u][g]);
-            const float corr = fast_exp2(m[g] - mx);
-            m[g] = mx;
-            l[g] *= corr;
-#pragma unroll
-            for (int e = 0; e < DPL; ++e) acc[g][e] *= corr;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float vf[DPL];
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) Chunk<T>::unpack(vr[u][j], &vf[j * VEC]);
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float p = fast_exp2(s[u][g] - m[g]);
-                l[g] += p;
-#pragma unroll
-                for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
-            }
-        }
-    }
-
-    // Merge the TPS token groups of the wave (lanes with equal `part`).
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float M = m[g];
-#pragma unroll
-        for (int off = LPT; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-        const float f = fast_exp2(m[g] - M);
-        l[g] *= f;
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[g][e] *= f;
-#pragma unroll
-        for (int off = LPT; off < 64; off <<= 1) {
-            l[g] += __shfl_xor(l[g], off, 64);
-#pragma unroll
-            for (int e = 0; e < DPL; ++e) acc[g][e] += __shfl_xor(acc[g][e], off, 64);
-        }
-        m[g] = M;
-    }
-
-    const bool direct = geo.nsplit == 1;
-    if (grp == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float inv = 1.0f / l[g];
-            float o[DPL];
-#pragma unroll
-            for (int e = 0; e < DPL; ++e) o[e] = acc[g][e] * inv;
-            const int64_t bh = (int64_t)b * a.Hq + hq0 + g;
-            if (direct) {
-                T* op = out + bh * D;
-#pragma unroll
-                for (int j = 0; j < NJ; ++j)
-                    *reinterpret_cast<uint4*>(op + (j * LPT + part) * VEC) = Chunk<T>::pack(&o[j * VEC]);
-            } else {
-                float* pp = a.part_o + (bh * a.S_max + split) * D;
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-#pragma unroll
-                    for (int e4 = 0; e4 < VEC; e4 += 4)
-                        *reinterpret_cast<float4*>(pp + (j * LPT + part) * VEC + e4) =
-                            make_float4(o[j * VEC + e4], o[j * VEC + e4 + 1], o[j * VEC + e4 + 2],
-                                        o[j * VEC + e4 + 3]);
-                }
-                if (part == 0) a.part_lse[bh * a.S_max + split] = m[g] + fast_log2(l[g]);
-            }
-        }
-    }
-    if (direct) return;
-    // The split that completes this (sequence, kv_head) merges all its partials.
-    int* counter = a.counters + (int64_t)b * a.Hq + hq0;
-    if (split_arrive_last(counter, geo.nsplit)) split_merge<T>(a, b, hq0, G, geo.nsplit, counter);
-}
 
 // Generic decode kernel: any head_dim <= 256, any group size, any page size.
 // One wave per (split, q_head, sequence); 64 keys per iteration, one key per
@@ -299,8 +120,52 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeArgs a) {
         if (d < D) pp[d] = acc[i] * inv;
     }
     if (lane == 0) a.part_lse[bh * a.S_max + split] = m + fast_log2(l);
-    int* counter = a.counters + bh;
-    if (split_arrive_last(counter, geo.nsplit)) split_merge<T>(a, b, hq, 1, geo.nsplit, counter);
+}
+
+// Merge of the split partials of one (sequence, q head), launched after the
+// split kernel (the reference's paged_attention_reduce_kernel,
+// src/kv_cache/paged_attention.cu:477-532, in normalised form:
+// out = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M)).  One wave; lane owns
+// dims lane + 64 i (i < MD); partials are fetched 8 splits at a time so a
+// merge costs ceil(nsplit / 8) memory round trips.
+template <typename T, int MD>
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
+    const int hq = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+    const SplitGeo geo = split_geo(a, b);
+    if (geo.nsplit <= 1) return;   // written directly by the split kernel
+    const int D = a.D, nsplit = geo.nsplit;
+    const int64_t bh = (int64_t)b * a.Hq + hq;
+    const float* lse = a.part_lse + bh * a.S_max;
+    const float* po = a.part_o + bh * a.S_max * D;
+    float mx = -INFINITY;
+    for (int s = lane; s < nsplit; s += 64) mx = fmaxf(mx, lse[s]);
+    const float M = wave_max(mx);
+    constexpr int SC = 8;
+    float W = 0.0f, o[MD];
+#pragma unroll
+    for (int i = 0; i < MD; ++i) o[i] = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += SC) {
+        float lv[SC], pv[SC][MD];
+#pragma unroll
+        for (int j = 0; j < SC; ++j) {
+            const int s = min(s0 + j, nsplit - 1);   // clamped reads; weight zeroed below
+            lv[j] = lse[s];
+#pragma unroll
+            for (int i = 0; i < MD; ++i) pv[j][i] = po[(int64_t)s * D + min(lane + 64 * i, D - 1)];
+        }
+#pragma unroll
+        for (int j = 0; j < SC; ++j) {
+            const float w = s0 + j < nsplit ? fast_exp2(lv[j] - M) : 0.0f;
+            W += w;
+#pragma unroll
+            for (int i = 0; i < MD; ++i) o[i] = fmaf(w, pv[j][i], o[i]);
+        }
+    }
+    T* out = reinterpret_cast<T*>(a.out) + bh * D;
+    const float inv = 1.0f / W;
+#pragma unroll
+    for (int i = 0; i < MD; ++i)
+        if (lane + 64 * i < D) out[lane + 64 * i] = Elem<T>::from_f32(o[i] * inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -327,15 +192,40 @@ DecodeFn pick_fast(int D, int G) {
     return nullptr;
 }
 
+template <int D>
+DecodeFn pick_mfma_f32_g(int G) {
+    switch (G) {
+        case 1: return decode_mfma_f32_kernel<D, 1>;
+        case 2: return decode_mfma_f32_kernel<D, 2>;
+        case 4: return decode_mfma_f32_kernel<D, 4>;
+        case 7: return decode_mfma_f32_kernel<D, 7>;
+        case 8: return decode_mfma_f32_kernel<D, 8>;
+        case 16: return decode_mfma_f32_kernel<D, 16>;
+    }
+    return nullptr;
+}
+
+// fp32 pools: the MFMA kernel (decode_mfma.h).
+DecodeFn pick_f32(int D, int G) {
+    if (D == 64) return pick_mfma_f32_g<64>(G);
+    if (D == 128) return pick_mfma_f32_g<128>(G);
+    return nullptr;
+}
+
 struct Plan {
     int S_max;
     int pps_auto;
     int fixed_S;
 };
 
-// Automatic split size: aim for roughly 8 resident waves per CU over the
-// whole batch (256 CUs), never below 4 pages (64 tokens) per split so that
-// partial traffic stays a few percent of the KV bytes.
+// Automatic split size (pages per split).  Only the longest length is known
+// on the host, so the batch is sized as if sequences averaged half of it:
+// about 4096 splits in total (16 waves per CU over 256 CUs), at least 4
+// pages (64 tokens) per split so partials stay a few percent of the KV
+// bytes, and at most kMaxAutoSplits splits per sequence so the merge that
+// closes a sequence stays short.
+constexpr int kMaxAutoSplits = 64;
+
 Plan make_plan(int B, int Hkv, int bs, int max_seq_len, int num_splits) {
     Plan p;
     int max_pages = (std::max(max_seq_len, 1) + bs - 1) / bs;
@@ -345,29 +235,31 @@ Plan make_plan(int B, int Hkv, int bs, int max_seq_len, int num_splits) {
         p.S_max = std::min(num_splits, max_pages);
     } else {
         p.fixed_S = 0;
-        const int64_t target_items = 256 * 8;
-        int64_t units = (int64_t)B * Hkv;
-        int64_t want = (target_items + units - 1) / units;   // splits per (seq, kv_head)
-        int pps = (int)std::max<int64_t>(4, (max_pages + want - 1) / want);
-        p.pps_auto = pps;
-        p.S_max = (max_pages + pps - 1) / pps;
+        // Split-kernel work-groups are 4 waves; aim for ~1280 of them (5 per
+        // CU, all resident at once), assuming sequences average half the
+        // longest.
+        const int64_t units = (int64_t)B * Hkv;
+        int64_t pps = ((int64_t)max_pages * units / 2 + 1279) / 1280;
+        const int64_t lo = std::max<int64_t>(4, (max_pages + kMaxAutoSplits - 1) / kMaxAutoSplits);
+        // At most 32 pages (512 tokens) per chunk unless the split cap forces
+        // it: a few long sequences in a batch of short ones (a lognormal mix)
+        // must still be spread over many work-groups.
+        const int64_t hi = std::max<int64_t>(lo, 32);
+        pps = std::min(std::max(pps, lo), hi);
+        p.pps_auto = (int)pps;
+        p.S_max = (int)((max_pages + pps - 1) / pps);
     }
     if (p.S_max < 1) p.S_max = 1;
     return p;
 }
 
-// Workspace: [counters: fixed kCounterBytes][lse B*Hq*S_max][o B*Hq*S_max*D].
-// The counter region has the same size and place for every call, so a
-// workspace reused across batch shapes never finds partial data where a
-// counter is expected (the counters are zero between calls).
-constexpr size_t kCounterBytes = 256 * 1024;
-constexpr int kMaxHeadRows = (int)(kCounterBytes / sizeof(int));   // B * Hq limit
-size_t counter_bytes(int, int) { return kCounterBytes; }
+// Workspace: [lse B*Hq*S_max, 256 B aligned][o B*Hq*S_max*D], fp32.
+size_t lse_bytes(size_t n) { return (n * sizeof(float) + 255) & ~(size_t)255; }
 
 size_t workspace_for(int B, int Hq, int D, const Plan& p) {
     if (p.S_max <= 1) return 0;
     size_t n = (size_t)B * Hq * p.S_max;
-    return counter_bytes(B, Hq) + ((n * sizeof(float) + 255) & ~(size_t)255) + n * D * sizeof(float);
+    return lse_bytes(n) + n * D * sizeof(float);
 }
 
 }  // namespace
@@ -410,9 +302,6 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
     if (max_seq_len > max_blocks_per_seq * block_size) max_seq_len = max_blocks_per_seq * block_size;
 
     Plan p = make_plan(num_seqs, num_kv_heads, block_size, max_seq_len, num_splits);
-    if (p.S_max > 1 && (int64_t)num_seqs * num_q_heads > kMaxHeadRows)
-        return set_error(LLKV_ERR_UNSUPPORTED, "%s: num_seqs * num_q_heads %lld exceeds %d", fn,
-                         (long long)num_seqs * num_q_heads, kMaxHeadRows);
     size_t need = workspace_for(num_seqs, num_q_heads, head_dim, p);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
         return set_error(LLKV_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn,
@@ -427,11 +316,8 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
     a.lens = seq_lens;
     size_t n = (size_t)num_seqs * num_q_heads * p.S_max;
     char* ws = reinterpret_cast<char*>(workspace);
-    a.counters = need ? reinterpret_cast<int*>(ws) : nullptr;
-    a.part_lse = need ? reinterpret_cast<float*>(ws + counter_bytes(num_seqs, num_q_heads)) : nullptr;
-    a.part_o = need ? reinterpret_cast<float*>(ws + counter_bytes(num_seqs, num_q_heads) +
-                                               ((n * sizeof(float) + 255) & ~(size_t)255))
-                    : nullptr;
+    a.part_lse = need ? reinterpret_cast<float*>(ws) : nullptr;
+    a.part_o = need ? reinterpret_cast<float*>(ws + lse_bytes(n)) : nullptr;
     a.B = num_seqs;
     a.Hq = num_q_heads;
     a.Hkv = num_kv_heads;
@@ -452,19 +338,35 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
                          ((size_t)num_kv_heads * head_dim * es) % 16 == 0;
     DecodeFn fast = nullptr;
     if (block_size == kPage && aligned) {
-        if (dtype == LLKV_DTYPE_F32) fast = pick_fast<float>(head_dim, G);
+        if (dtype == LLKV_DTYPE_F32) fast = pick_f32(head_dim, G);
         else if (dtype == LLKV_DTYPE_F16) fast = pick_fast<_Float16>(head_dim, G);
         else if (dtype == LLKV_DTYPE_BF16) fast = pick_fast<bf16_t>(head_dim, G);
     }
     if (fast) {
         dim3 grid(p.S_max, num_kv_heads, num_seqs);
-        fast<<<grid, 64, 0, st>>>(a);
+        fast<<<grid, 64 * kDecodeWaves, 0, st>>>(a);
     } else {
         dim3 grid(p.S_max, num_q_heads, num_seqs);
         if (dtype == LLKV_DTYPE_F32) decode_generic_kernel<float><<<grid, 64, 0, st>>>(a);
         else if (dtype == LLKV_DTYPE_F16) decode_generic_kernel<_Float16><<<grid, 64, 0, st>>>(a);
         else decode_generic_kernel<bf16_t><<<grid, 64, 0, st>>>(a);
     }
-    return check_launch(fn);
+    if (int e = check_launch(fn)) return e;
+    if (p.S_max > 1) {
+        dim3 grid(num_q_heads, num_seqs);
+        const bool wide = head_dim > 128;
+        if (dtype == LLKV_DTYPE_F32) {
+            if (wide) decode_merge_kernel<float, 4><<<grid, 64, 0, st>>>(a);
+            else decode_merge_kernel<float, 2><<<grid, 64, 0, st>>>(a);
+        } else if (dtype == LLKV_DTYPE_F16) {
+            if (wide) decode_merge_kernel<_Float16, 4><<<grid, 64, 0, st>>>(a);
+            else decode_merge_kernel<_Float16, 2><<<grid, 64, 0, st>>>(a);
+        } else {
+            if (wide) decode_merge_kernel<bf16_t, 4><<<grid, 64, 0, st>>>(a);
+            else decode_merge_kernel<bf16_t, 2><<<grid, 64, 0, st>>>(a);
+        }
+        if (int e = check_launch(fn)) return e;
+    }
+    return LLKV_OK;
 }
 

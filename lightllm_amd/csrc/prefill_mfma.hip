@@ -43,6 +43,7 @@ struct Smem {
     static constexpr int VPAD = BN + 8;   // halves per V^T row
     uint16_t k[2][BN * KPAD];
     uint16_t vt[2][D * VPAD];
+    int pages[1024];   // page ids [tbase, tbase + 1024) of the sequence
 };
 
 template <typename T, int D>
@@ -112,6 +113,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     float lsum[2] = {0.f, 0.f};
 
     // ---- staging: global -> registers -> LDS -----------------------------
+    int tbase = 0;   // first page id held in sm.pages
     uint4 kreg[KCH_T];
     uint4 vreg[VT_T][2];
     auto load_tile = [&](int t) {
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             const int ch = tid + 256 * j;
             const int key = ch / (D / 8), c = ch % (D / 8);
             const int page = min((key0 + key) >> 4, last_page);
-            const int64_t row = (int64_t)max(bt[page], 0) * kPage + ((key0 + key) & 15);
+            const int64_t row = (int64_t)max(sm.pages[page - tbase], 0) * kPage + ((key0 + key) & 15);
             kreg[j] = *reinterpret_cast<const uint4*>(kg + row * row_elems + c * 8);
         }
 #pragma unroll
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             const int kp = task % (BN / 2), c = task / (BN / 2);
             const int key = key0 + 2 * kp;
             const int page = min(key >> 4, last_page);
-            const int64_t row = (int64_t)max(bt[page], 0) * kPage + (key & 15);
+            const int64_t row = (int64_t)max(sm.pages[page - tbase], 0) * kPage + (key & 15);
             vreg[j][0] = *reinterpret_cast<const uint4*>(vg + row * row_elems + c * 8);
             vreg[j][1] = *reinterpret_cast<const uint4*>(vg + (row + 1) * row_elems + c * 8);
         }
@@ -158,7 +160,14 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         }
     };
 
+    // Page ids live in LDS so that no K/V load waits behind a table load.
+    auto stage_pages = [&](int base) {
+        tbase = base;
+        for (int i = tid; i < 1024; i += 256) sm.pages[i] = bt[min(base + i, last_page)];
+        __syncthreads();
+    };
     if (ntiles > 0) {
+        stage_pages(0);
         load_tile(0);
         store_tile(0);
     }
@@ -166,7 +175,13 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
-        if (t + 1 < ntiles) load_tile(t + 1);
+        if (t + 1 < ntiles) {
+            // tile t+1 covers pages [4(t+1), 4(t+1)+4); restage when they leave the window
+            // (uniform branch; every earlier read of sm.pages preceded the last barrier)
+            if (4 * (t + 1) + 4 > tbase + 1024) stage_pages(4 * (t + 1));
+            load_tile(t + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // next tile's loads issue before this tile's MFMAs
 
         // ---- S^T = K Q^T over the 64 keys: 4 key tiles x 2 query tiles ----
         f32x4 s[4][2];

@@ -209,8 +209,8 @@ _WS: dict = {}
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
-    """Zero-filled decode workspace, cached per device and grown on demand (the kernels
-    leave its split counters at zero after every call)."""
+    """Decode workspace (split partials), cached per device and grown on demand.  Calls
+    that share it must be ordered on one stream."""
     key = str(device)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
