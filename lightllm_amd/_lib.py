@@ -103,3 +103,15 @@ def check(status: int) -> None:
     if status != 0:
         msg = lib().llkv_last_error().decode(errors="replace")
         raise LLKVError(status, msg)
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def last_error() -> str:
+    return lib().llkv_last_error().decode(errors="replace")
+
+
+def status_string(status: int) -> str:
+    return lib().llkv_status_string(status).decode(errors="replace")
