@@ -15,6 +15,14 @@ reference's reconstruct_kv + cpu_attention, on this host), and configuration
 4's paged prefill as MFMA utilisation.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+
+Profiling helpers (the commands that produce the summaries under profiles/):
+  python bench.py --calibrate-copy          a plain 256 MiB device copy, the
+                                            reference point for FETCH_SIZE /
+                                            WRITE_SIZE scaling
+  python bench.py --rocprof-summary DIR     per-kernel averages of the rocprofv3
+                                            CSV files (kernel trace, counters)
+                                            found under DIR
 """
 from __future__ import annotations
 
@@ -30,6 +38,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+COPY_CAL_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_cfg2_traffic.txt")
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 METRIC = "paged decode µs/layer + achieved HBM GB/s (% peak) at B=64; prefill MFMA %"
 
@@ -188,6 +198,71 @@ def cpu_baseline(dec, budget_s: float):
             "cpu_model": cpu_model(), "nproc": os.cpu_count()}
 
 
+def calibrate_copy(torch) -> None:
+    """Plain device-to-device copy of COPY_CAL_BYTES, five times: under rocprofv3 --pmc its
+    FETCH_SIZE / WRITE_SIZE per dispatch (KiB) against the known bytes gives the scale
+    factor applied to the decode kernels' counters."""
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_CAL_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read": COPY_CAL_BYTES,
+                      "bytes_written": COPY_CAL_BYTES, "launches": 5}))
+
+
+def rocprof_summary(path: str) -> None:
+    """Print per-kernel averages from rocprofv3 CSV output under `path`: kernel-trace
+    durations (*kernel_trace.csv) and counter values (*counter_collection.csv)."""
+    import csv
+    import glob
+    import re
+    import subprocess
+
+    def short(n):
+        if n.startswith("_Z"):
+            try:
+                n = subprocess.run(["c++filt", n], capture_output=True, text=True).stdout.strip() or n
+            except OSError:
+                pass
+        n = n.replace("(anonymous namespace)::", "")
+        return re.sub(r"\(.*", "", n).replace("void ", "").strip()[:100]
+    for f in sorted(glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True)):
+        agg = {}
+        for r in csv.DictReader(open(f)):
+            d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            agg.setdefault(short(r["Kernel_Name"]), []).append(d)
+        print(f"# kernel trace: {os.path.relpath(f, path)}")
+        print(f"{'calls':>7} {'avg_us':>9} {'median_us':>9} {'min_us':>8} {'max_us':>8}  kernel")
+        for n, ds in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+            print(f"{len(ds):7d} {statistics.fmean(ds):9.2f} {statistics.median(ds):9.2f} "
+                  f"{min(ds):8.2f} {max(ds):8.2f}  {n}")
+    for f in sorted(glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True)):
+        agg = {}
+        for r in csv.DictReader(open(f)):
+            key = (short(r["Kernel_Name"]), r["Counter_Name"])
+            agg.setdefault(key, []).append(float(r["Counter_Value"]))
+        print(f"# counters: {os.path.relpath(f, path)}")
+        print(f"{'dispatches':>10} {'mean_per_dispatch':>18}  counter  kernel")
+        for (n, c), v in sorted(agg.items()):
+            print(f"{len(v):10d} {statistics.fmean(v):18.1f}  {c}  {n}")
+
+
+def read_traffic():
+    """HBM bytes per decode call measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, scaled by
+    the copy calibration), recorded in profiles/decode_cfg2_traffic.txt as a line
+    'traffic_bytes_per_call: N'."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_call:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,13 +272,21 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--rocprof-summary", metavar="DIR")
     args = ap.parse_args()
+    if args.rocprof_summary:
+        rocprof_summary(args.rocprof_summary)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build's path has no multi-GPU "
               "component (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
     import torch
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
     from lightllm_amd import kv_cache as kc
     from lightllm_amd import workloads as wl
 
@@ -212,6 +295,7 @@ def main():
     cpu = None if args.no_cpu_baseline else cpu_baseline(dec, args.cpu_budget)
 
     step_us = dec["step_ms"] * 1e3
+    traffic = read_traffic()
     value = dec["decode_bytes"] / (dec["decode_us_mean"] * 1e-6) / 1e9
     step_gbs = (dec["decode_bytes"] + dec["append_bytes"]) / (step_us * 1e-6) / 1e9
     line = {
@@ -235,9 +319,11 @@ def main():
         "decode_kernel_us": round(dec["decode_us_mean"], 2),
         "decode_GBps_page_granular": round(dec["decode_bytes_pages"] / (dec["decode_us_mean"] * 1e-6) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_fast_kernel<float,64,7> (split merge fused)",
-                     "bytes_per_launch": dec["decode_bytes"]},
+                     "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "llkv_paged_decode = decode_mfma_f32_kernel<64,7> (split) + "
+                               "decode_merge_kernel<float,1> (split merge)",
+                     "bytes_per_launch": dec["decode_bytes"],
+                     "timing": "HIP events on the launch stream around each llkv_paged_decode call"},
         "parity_ok": dec["parity_ok"],
         "cpu_baseline": cpu,
     }

@@ -108,12 +108,17 @@ int llkv_gather(void* k_dst, void* v_dst, const void* k_pool,
  * seq_lens   : device int32 [num_seqs]; sequence b attends positions [0, len).
  * max_seq_len: host-side upper bound of every seq_lens[b] (sizes the grid
  *              without the reference's device-to-host read).
- * num_splits : 0 = automatic split of each sequence's KV range;
+ * num_splits : 0 = automatic: the batch's pages are shared equally among as
+ *              many work-groups as the GPU holds at once, whatever the length
+ *              mix (up to 1024 sequences; larger batches use 8-page splits);
  *              S > 0 = the reference's fixed split (S ranges of ceil(n/S) pages).
  * scale      : softmax scale (the reference uses 1/sqrt(head_dim)).
  * workspace  : device memory of at least llkv_paged_decode_workspace_size()
  *              bytes (may be NULL when that size is 0); it holds the split
- *              partials.  Calls sharing one workspace must not overlap.
+ *              partials and arrival counters.  It must be zero-filled before
+ *              its first use; every call leaves the counters zero again, so
+ *              one workspace serves any later call.  Calls sharing one
+ *              workspace must not overlap.
  * ------------------------------------------------------------------------ */
 size_t llkv_paged_decode_workspace_size(int num_seqs, int num_q_heads,
                                         int num_kv_heads, int head_dim,

@@ -17,15 +17,22 @@
 //    (quad_perm, row_half_mirror, row_mirror); each token group keeps its own
 //    running (max, sum, acc) so no cross-group traffic happens until the end
 //    of the split, where the groups are merged by log-sum-exp with shuffles.
-//  * Split-K is per sequence: a sequence of n pages gets ceil(n/pps) splits
-//    (automatic) or the reference's S ranges of ceil(n/S) pages (fixed), so
-//    short sequences in a mixed batch launch no idle split.  Partials are
-//    merged by log-sum-exp in a small second kernel; a sequence with one
-//    split writes the output directly.
+//  * Two schedules.  Fixed split (num_splits = S > 0): the reference's S
+//    ranges of ceil(n/S) pages per sequence, one work-group per (split, kv
+//    head, sequence).  Balanced (num_splits = 0): as many work-groups as the
+//    GPU holds at once, each taking an equal share of the batch's pages
+//    whatever the length mix (attn_common.h), so no work-group waits for a
+//    slot and none runs long.  Partials are merged by log-sum-exp in a small
+//    second kernel; a (sequence, kv head) computed by one work-group writes
+//    its output directly.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "attn_common.h"
 #include "decode_fast.h"
@@ -122,50 +129,190 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeArgs a) {
     if (lane == 0) a.part_lse[bh * a.S_max + split] = m + fast_log2(l);
 }
 
-// Merge of the split partials of one (sequence, q head), launched after the
-// split kernel (the reference's paged_attention_reduce_kernel,
-// src/kv_cache/paged_attention.cu:477-532, in normalised form:
-// out = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M)).  One wave; lane owns
-// dims lane + 64 i (i < MD); partials are fetched 8 splits at a time so a
-// merge costs ceil(nsplit / 8) memory round trips.
-template <typename T, int MD>
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
-    const int hq = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-    const SplitGeo geo = split_geo(a, b);
-    if (geo.nsplit <= 1) return;   // written directly by the split kernel
-    const int D = a.D, nsplit = geo.nsplit;
-    const int64_t bh = (int64_t)b * a.Hq + hq;
-    const float* lse = a.part_lse + bh * a.S_max;
-    const float* po = a.part_o + bh * a.S_max * D;
-    float mx = -INFINITY;
-    for (int s = lane; s < nsplit; s += 64) mx = fmaxf(mx, lse[s]);
-    const float M = wave_max(mx);
-    constexpr int SC = 8;
-    float W = 0.0f, o[MD];
+// Log-sum-exp merge of `count` partials of one (sequence, q head): entry j
+// is the normalised row po + j * po_step (D floats) with log2-sum-exp2
+// pl[j * pl_step]; live(j) false skips an entry.  One wave; lane owns dims
+// lane + 64 i; entries are fetched kMergeBatch at a time with a running
+// maximum, so a merge costs ceil(count / kMergeBatch) memory round trips.
+// The reference's paged_attention_reduce_kernel
+// (src/kv_cache/paged_attention.cu:477-532) computes the same sum in
+// unnormalised form: out = sum_j 2^(lse_j - M) o_j / sum_j 2^(lse_j - M).
+constexpr int kMergeBatch = 16;
+
+template <typename T, int MD, class Live>
+__device__ inline void merge_partials(const float* po, int64_t po_step, const float* pl,
+                                      int64_t pl_step, int count, int D, Live live, T* out) {
+    const int lane = threadIdx.x & 63;
+    float M = -INFINITY, W = 0.0f, o[MD];
 #pragma unroll
     for (int i = 0; i < MD; ++i) o[i] = 0.0f;
-    for (int s0 = 0; s0 < nsplit; s0 += SC) {
-        float lv[SC], pv[SC][MD];
+    for (int j0 = 0; j0 < count; j0 += kMergeBatch) {
+        float lv[kMergeBatch], pv[kMergeBatch][MD];
 #pragma unroll
-        for (int j = 0; j < SC; ++j) {
-            const int s = min(s0 + j, nsplit - 1);   // clamped reads; weight zeroed below
-            lv[j] = lse[s];
+        for (int j = 0; j < kMergeBatch; ++j) {
+            const bool ok = j0 + j < count && live(j0 + j);
+            const int64_t jj = j0 + j;
+            lv[j] = ok ? pl[jj * pl_step] : -INFINITY;
 #pragma unroll
-            for (int i = 0; i < MD; ++i) pv[j][i] = po[(int64_t)s * D + min(lane + 64 * i, D - 1)];
+            for (int i = 0; i < MD; ++i)
+                pv[j][i] = ok ? po[jj * po_step + min(lane + 64 * i, D - 1)] : 0.0f;
         }
+        float mb = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < SC; ++j) {
-            const float w = s0 + j < nsplit ? fast_exp2(lv[j] - M) : 0.0f;
+        for (int j = 0; j < kMergeBatch; ++j) mb = fmaxf(mb, lv[j]);
+        const float Mn = fmaxf(M, mb);
+        if (Mn == -INFINITY) continue;
+        const float sc = fast_exp2(M - Mn);
+        W *= sc;
+#pragma unroll
+        for (int i = 0; i < MD; ++i) o[i] *= sc;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+            const float w = fast_exp2(lv[j] - Mn);
             W += w;
 #pragma unroll
             for (int i = 0; i < MD; ++i) o[i] = fmaf(w, pv[j][i], o[i]);
         }
+        M = Mn;
     }
-    T* out = reinterpret_cast<T*>(a.out) + bh * D;
     const float inv = 1.0f / W;
 #pragma unroll
     for (int i = 0; i < MD; ++i)
         if (lane + 64 * i < D) out[lane + 64 * i] = Elem<T>::from_f32(o[i] * inv);
+}
+
+struct AllLive {
+    __device__ bool operator()(int) const { return true; }
+};
+
+// Merge of the fixed split schedule: grid (Hq, B), one wave each.
+template <typename T, int MD>
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
+    const int hq = blockIdx.x, b = blockIdx.y;
+    const SplitGeo geo = split_geo(a, b);
+    if (geo.nsplit <= 1) return;   // written directly by the split kernel
+    const int64_t bh = (int64_t)b * a.Hq + hq;
+    merge_partials<T, MD>(a.part_o + bh * a.S_max * a.D, a.D, a.part_lse + bh * a.S_max, 1,
+                          geo.nsplit, a.D, AllLive(), reinterpret_cast<T*>(a.out) + bh * a.D);
+}
+
+// Work-groups of the balanced schedule that hold pages (a work-group's share
+// is empty when the batch has fewer page-units than work-groups).
+struct LiveWG {
+    int64_t w0, T;
+    int nwg;
+    __device__ bool operator()(int j) const { return wg_nonempty(w0 + j, T, nwg); }
+};
+
+// Fixed split schedule: grid (S_max, Hkv, B), 4 waves per work-group, one
+// segment each.
+template <class Body>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Body::kWavesPerEU)))
+void decode_split_kernel(DecodeArgs a) {
+    __shared__ typename Body::Smem sm;
+    __shared__ SegDesc segs[1];
+    using T = typename Body::T;
+    LLKV_TRACE_POINT(0);
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const SplitGeo geo = split_geo(a, b);
+    const int hq0 = kvh * Body::GQ;
+    if (geo.npages == 0) {   // empty sequence: zeros, as the reference (:224-227)
+        if (split == 0) {
+            T* out = reinterpret_cast<T*>(a.out) + ((int64_t)b * a.Hq + hq0) * Body::HD;
+            for (int i = threadIdx.x; i < Body::GQ * Body::HD; i += blockDim.x)
+                out[i] = Elem<T>::from_f32(0.0f);
+        }
+        return;
+    }
+    if (split >= geo.nsplit) return;
+    if (threadIdx.x == 0) {
+        SegDesc& d = segs[0];
+        d.b = b;
+        d.kvh = kvh;
+        d.pg_begin = split * geo.pps;
+        d.npages = min(geo.pps, geo.npages - d.pg_begin);
+        d.cum = 0;
+        d.tok_end = min((d.pg_begin + d.npages) * kPage, geo.L);
+        d.direct = geo.nsplit == 1;
+        const int64_t bh0 = (int64_t)b * a.Hq + hq0;
+        d.po_off = (bh0 * a.S_max + split) * a.D;
+        d.pl_off = bh0 * a.S_max + split;
+    }
+    __syncthreads();
+    Body::round(a, sm, segs, 1, (int64_t)a.S_max * a.D, a.S_max);
+}
+
+// Balanced schedule: grid (nwg), 4 waves per work-group.  Every work-group
+// scans the lengths itself (the batch is at most kBalanceMaxB sequences) and
+// cuts its share into segments, run kSegMax segments per round.  A unit
+// (sequence, kv head) inside one share is written directly; the others are
+// merged by decode_merge_balanced_kernel.  Work-group 0 stores the page
+// prefix sums for that kernel; empty sequences get zeros from the work-group
+// with their index modulo nwg.
+template <class Body>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Body::kWavesPerEU)))
+void decode_balanced_kernel(DecodeArgs a) {
+    using T = typename Body::T;
+    constexpr int D = Body::HD;
+    __shared__ typename Body::Smem sm;
+    __shared__ int sP[kBalanceMaxB + 1];
+    __shared__ int sL[kBalanceMaxB];
+    __shared__ SegDesc segs[Body::kSegMax];
+    __shared__ int s_n;
+    __shared__ int64_t s_next;
+    LLKV_TRACE_POINT(0);
+    scan_pages(a, sP, sL);
+    LLKV_TRACE_POINT(4);
+    const int tid = threadIdx.x;
+    if (blockIdx.x == 0)
+        for (int i = tid; i <= a.B; i += blockDim.x) a.plan[i] = sP[i];
+    const int64_t T_ = (int64_t)a.Hkv * sP[a.B];
+    const int64_t wg = blockIdx.x;
+    for (int b = (int)wg; b < a.B; b += a.nwg) {   // the reference's seq_len == 0 rule (:224-227)
+        if (sP[b + 1] != sP[b]) continue;
+        T* out = reinterpret_cast<T*>(a.out) + (int64_t)b * a.Hq * D;
+        for (int i = tid; i < a.Hq * D; i += blockDim.x) out[i] = Elem<T>::from_f32(0.0f);
+    }
+    const int64_t r1 = share_begin(wg + 1, T_, a.nwg);
+    int64_t p = share_begin(wg, T_, a.nwg);
+    while (p < r1) {
+        if (tid == 0) {
+            int n = 0;
+            s_next = build_segments(a, sP, sL, p, r1, wg, Body::kSegMax, segs, &n);
+            s_n = n;
+        }
+        __syncthreads();
+        const int n = s_n;
+        p = s_next;
+        Body::round(a, sm, segs, n, D, 1);   // ends with a barrier
+    }
+}
+
+// Merge of the balanced schedule: grid (Hq, B), one wave each.  Unit
+// (b, kvh) spans positions [s, e); its segments are those of work-groups
+// wg_of(s) .. wg_of(e - 1), with ids w + u.
+template <typename T, int MD>
+__global__ __launch_bounds__(64) void decode_merge_balanced_kernel(DecodeArgs a) {
+    const int hq = blockIdx.x, b = blockIdx.y;
+    const int G = a.Hq / a.Hkv;
+    const int kvh = hq / G, h = hq - kvh * G;
+    const int D = a.D;
+    const int Pb = a.plan[b];
+    const int np = a.plan[b + 1] - Pb;
+    if (np == 0) return;   // zeros written by the split kernel
+    const int64_t T_ = (int64_t)a.Hkv * a.plan[a.B];
+    const int64_t s = (int64_t)a.Hkv * Pb + (int64_t)kvh * np;
+    const int64_t wf = wg_of(s, T_, a.nwg), wl = wg_of(s + np - 1, T_, a.nwg);
+    if (wf == wl) return;   // written directly
+    const int64_t seg0 = wf + (int64_t)b * a.Hkv + kvh;
+    T* out = reinterpret_cast<T*>(a.out) + ((int64_t)b * a.Hq + hq) * D;
+    const float* po = a.part_o + (seg0 * G + h) * D;
+    const float* pl = a.part_lse + seg0 * G + h;
+    const int cnt = (int)(wl - wf + 1);
+    if (T_ >= a.nwg)   // every work-group holds pages: all entries live
+        merge_partials<T, MD>(po, (int64_t)G * D, pl, G, cnt, D, AllLive(), out);
+    else
+        merge_partials<T, MD>(po, (int64_t)G * D, pl, G, cnt, D, LiveWG{wf, T_, a.nwg}, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -173,43 +320,56 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 typedef void (*DecodeFn)(DecodeArgs);
 
+struct Kernels {
+    DecodeFn split = nullptr;
+    DecodeFn balanced = nullptr;
+};
+
+template <class Body>
+Kernels kernels_of() {
+    Kernels k;
+    k.split = decode_split_kernel<Body>;
+    k.balanced = decode_balanced_kernel<Body>;
+    return k;
+}
+
 template <typename T, int D>
-DecodeFn pick_fast_g(int G) {
+Kernels pick_fast_g(int G) {
     switch (G) {
-        case 1: return decode_fast_kernel<T, D, 1>;
-        case 2: return decode_fast_kernel<T, D, 2>;
-        case 4: return decode_fast_kernel<T, D, 4>;
-        case 7: return decode_fast_kernel<T, D, 7>;
-        case 8: return decode_fast_kernel<T, D, 8>;
+        case 1: return kernels_of<FastDecode<T, D, 1>>();
+        case 2: return kernels_of<FastDecode<T, D, 2>>();
+        case 4: return kernels_of<FastDecode<T, D, 4>>();
+        case 7: return kernels_of<FastDecode<T, D, 7>>();
+        case 8: return kernels_of<FastDecode<T, D, 8>>();
     }
-    return nullptr;
+    return Kernels();
 }
 
 template <typename T>
-DecodeFn pick_fast(int D, int G) {
+Kernels pick_fast(int D, int G) {
     if (D == 64) return pick_fast_g<T, 64>(G);
     if (D == 128) return pick_fast_g<T, 128>(G);
-    return nullptr;
+    return Kernels();
 }
 
 template <int D>
-DecodeFn pick_mfma_f32_g(int G) {
+Kernels pick_mfma_f32_g(int G) {
     switch (G) {
-        case 1: return decode_mfma_f32_kernel<D, 1>;
-        case 2: return decode_mfma_f32_kernel<D, 2>;
-        case 4: return decode_mfma_f32_kernel<D, 4>;
-        case 7: return decode_mfma_f32_kernel<D, 7>;
-        case 8: return decode_mfma_f32_kernel<D, 8>;
-        case 16: return decode_mfma_f32_kernel<D, 16>;
+        case 1: return kernels_of<MfmaF32Decode<D, 1>>();
+        case 2: return kernels_of<MfmaF32Decode<D, 2>>();
+        case 4: return kernels_of<MfmaF32Decode<D, 4>>();
+        case 7: return kernels_of<MfmaF32Decode<D, 7>>();
+        case 8: return kernels_of<MfmaF32Decode<D, 8>>();
+        case 16: return kernels_of<MfmaF32Decode<D, 16>>();
     }
-    return nullptr;
+    return Kernels();
 }
 
-// fp32 pools: the MFMA kernel (decode_mfma.h).
-DecodeFn pick_f32(int D, int G) {
+// fp32 pools: the MFMA body (decode_mfma.h).
+Kernels pick_f32(int D, int G) {
     if (D == 64) return pick_mfma_f32_g<64>(G);
     if (D == 128) return pick_mfma_f32_g<128>(G);
-    return nullptr;
+    return Kernels();
 }
 
 struct Plan {
@@ -218,15 +378,14 @@ struct Plan {
     int fixed_S;
 };
 
-// Automatic split size (pages per split).  Only the longest length is known
-// on the host, so the batch is sized as if sequences averaged half of it:
-// about 4096 splits in total (16 waves per CU over 256 CUs), at least 4
-// pages (64 tokens) per split so partials stay a few percent of the KV
-// bytes, and at most kMaxAutoSplits splits per sequence so the merge that
-// closes a sequence stays short.
+// Split size of the fixed schedule when num_splits = 0 but the balanced one
+// does not apply (odd shapes, more than kBalanceMaxB sequences): 8 pages per
+// split, larger for long contexts so one sequence has at most kMaxAutoSplits
+// partials to merge.
+constexpr int kAutoPps = 8;
 constexpr int kMaxAutoSplits = 64;
 
-Plan make_plan(int B, int Hkv, int bs, int max_seq_len, int num_splits) {
+Plan make_plan(int bs, int max_seq_len, int num_splits) {
     Plan p;
     int max_pages = (std::max(max_seq_len, 1) + bs - 1) / bs;
     if (num_splits > 0) {
@@ -235,31 +394,110 @@ Plan make_plan(int B, int Hkv, int bs, int max_seq_len, int num_splits) {
         p.S_max = std::min(num_splits, max_pages);
     } else {
         p.fixed_S = 0;
-        // Split-kernel work-groups are 4 waves; aim for ~1280 of them (5 per
-        // CU, all resident at once), assuming sequences average half the
-        // longest.
-        const int64_t units = (int64_t)B * Hkv;
-        int64_t pps = ((int64_t)max_pages * units / 2 + 1279) / 1280;
-        const int64_t lo = std::max<int64_t>(4, (max_pages + kMaxAutoSplits - 1) / kMaxAutoSplits);
-        // At most 32 pages (512 tokens) per chunk unless the split cap forces
-        // it: a few long sequences in a batch of short ones (a lognormal mix)
-        // must still be spread over many work-groups.
-        const int64_t hi = std::max<int64_t>(lo, 32);
-        pps = std::min(std::max(pps, lo), hi);
-        p.pps_auto = (int)pps;
-        p.S_max = (int)((max_pages + pps - 1) / pps);
+        const int pps = std::max(kAutoPps, (max_pages + kMaxAutoSplits - 1) / kMaxAutoSplits);
+        p.pps_auto = pps;
+        p.S_max = (max_pages + pps - 1) / pps;
     }
     if (p.S_max < 1) p.S_max = 1;
     return p;
 }
 
-// Workspace: [lse B*Hq*S_max, 256 B aligned][o B*Hq*S_max*D], fp32.
-size_t lse_bytes(size_t n) { return (n * sizeof(float) + 255) & ~(size_t)255; }
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-size_t workspace_for(int B, int Hq, int D, const Plan& p) {
+// Fixed schedule workspace: [lse B*Hq*S_max, 256 B aligned][o B*Hq*S_max*D], fp32.
+size_t fixed_workspace(int B, int Hq, int D, const Plan& p) {
     if (p.S_max <= 1) return 0;
     size_t n = (size_t)B * Hq * p.S_max;
-    return lse_bytes(n) + n * D * sizeof(float);
+    return align256(n * sizeof(float)) + n * D * sizeof(float);
+}
+
+// Balanced schedule workspace: [plan int32 B+1][lse E*G][o E*G*D], each part
+// 256 B aligned, E = kBalanceMaxWG + B*Hkv segments (the largest id + 1).
+struct BalancedWs {
+    size_t plan_off, lse_off, o_off, total;
+};
+
+BalancedWs balanced_workspace(int B, int Hq, int Hkv, int D) {
+    const size_t E = (size_t)kBalanceMaxWG + (size_t)B * Hkv;
+    const size_t G = Hq / Hkv;
+    BalancedWs w;
+    w.plan_off = 0;
+    w.lse_off = align256((size_t)(B + 1) * sizeof(int));
+    w.o_off = w.lse_off + align256(E * G * sizeof(float));
+    w.total = w.o_off + E * G * D * sizeof(float);
+    return w;
+}
+
+bool balanced_eligible(int B) { return B <= kBalanceMaxB; }
+
+// Work-groups of kernel `fn` (256 threads) the current device holds at once:
+// compute units x resident work-groups per unit, cached per (device, kernel).
+int resident_wgs(DecodeFn fn) {
+    static std::mutex mu;
+    static std::map<std::pair<int, DecodeFn>, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({dev, fn});
+    if (it != cache.end()) return it->second;
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
+                                                     64 * kDecodeWaves, 0) != hipSuccess ||
+        per_cu <= 0)
+        per_cu = 1;
+    const int cap = std::max(1, cus * per_cu);
+    cache[{dev, fn}] = cap;
+    return cap;
+}
+
+// Work-groups of the balanced schedule: one resident set (more only adds a
+// second, partly idle round), capped by kBalanceMaxWG and by one page-unit
+// per wave.
+int balanced_wgs(DecodeFn fn, int64_t page_units_bound) {
+    const int cap = std::min(kBalanceMaxWG, resident_wgs(fn));
+    const int64_t by_work = std::max<int64_t>(1, (page_units_bound + kDecodeWaves - 1) / kDecodeWaves);
+    return (int)std::max<int64_t>(1, std::min<int64_t>(cap, by_work));
+}
+
+// Automatic schedule.  With few (sequence, kv head) units against the
+// resident work-group count, fixed splits of each unit fill the GPU in one
+// pass (S ~ 0.8 x resident / units; 1 KB-page reads per wave stay long enough
+// to keep the loads streaming); with many units (a large batch of uneven
+// lengths) the balanced schedule shares the pages equally instead.
+constexpr int kAutoMaxSplits = 64;
+
+struct AutoChoice {
+    bool balanced;
+    int splits;   // fixed schedule: S
+};
+
+AutoChoice auto_schedule(const Kernels& ks, int B, int Hkv, int max_pages) {
+    AutoChoice c{false, 0};
+    const int64_t units = (int64_t)B * Hkv;
+    const int cap = resident_wgs(ks.split);
+    if (ks.balanced != nullptr && balanced_eligible(B) && units * 4 >= cap) {
+        c.balanced = true;
+        return c;
+    }
+    int64_t S = (cap * 4 / 5 + units - 1) / units;
+    S = std::max<int64_t>(1, std::min<int64_t>({S, (int64_t)kAutoMaxSplits, (int64_t)std::max(1, max_pages)}));
+    c.splits = (int)S;
+    return c;
+}
+
+template <typename T, int MD>
+void launch_merge_md(bool balanced, dim3 grid, hipStream_t st, const DecodeArgs& a) {
+    if (balanced) decode_merge_balanced_kernel<T, MD><<<grid, 64, 0, st>>>(a);
+    else decode_merge_kernel<T, MD><<<grid, 64, 0, st>>>(a);
+}
+
+template <typename T>
+void launch_merge(bool balanced, int D, dim3 grid, hipStream_t st, const DecodeArgs& a) {
+    if (D <= 64) launch_merge_md<T, 1>(balanced, grid, st, a);
+    else if (D <= 128) launch_merge_md<T, 2>(balanced, grid, st, a);
+    else launch_merge_md<T, 4>(balanced, grid, st, a);
 }
 
 }  // namespace
@@ -272,10 +510,19 @@ extern "C" size_t llkv_paged_decode_workspace_size(int num_seqs, int num_q_heads
                                                    int block_size, int max_seq_len,
                                                    int num_splits) {
     if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
-        block_size <= 0)
+        block_size <= 0 || num_q_heads % num_kv_heads != 0)
         return 0;
-    Plan p = make_plan(num_seqs, num_kv_heads, block_size, max_seq_len, num_splits);
-    return workspace_for(num_seqs, num_q_heads, head_dim, p);
+    Plan p = make_plan(block_size, max_seq_len, num_splits);
+    size_t need = fixed_workspace(num_seqs, num_q_heads, head_dim, p);
+    if (num_splits == 0) {
+        // the automatic choice may be any fixed split up to kAutoMaxSplits, or balanced
+        const int max_pages = (std::max(max_seq_len, 1) + block_size - 1) / block_size;
+        Plan f = make_plan(block_size, max_seq_len, std::min(kAutoMaxSplits, max_pages));
+        need = std::max(need, fixed_workspace(num_seqs, num_q_heads, head_dim, f));
+        if (balanced_eligible(num_seqs))
+            need = std::max(need, balanced_workspace(num_seqs, num_q_heads, num_kv_heads, head_dim).total);
+    }
+    return need;
 }
 
 extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
@@ -300,12 +547,28 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
         return set_error(LLKV_ERR_INVALID, "%s: null pointer", fn);
     if (max_seq_len < 0) max_seq_len = 0;
     if (max_seq_len > max_blocks_per_seq * block_size) max_seq_len = max_blocks_per_seq * block_size;
+    if ((int64_t)num_seqs * max_blocks_per_seq > INT32_MAX)
+        return set_error(LLKV_ERR_UNSUPPORTED, "%s: block table too large", fn);
 
-    Plan p = make_plan(num_seqs, num_kv_heads, block_size, max_seq_len, num_splits);
-    size_t need = workspace_for(num_seqs, num_q_heads, head_dim, p);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-        return set_error(LLKV_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn,
-                         workspace_bytes, need);
+    const int G = num_q_heads / num_kv_heads;
+    // The tuned bodies need 16-token pages, 16-byte aligned rows and pointers.
+    const size_t es = dtype_bytes(dtype);
+    const bool aligned = (((uintptr_t)q | (uintptr_t)out | (uintptr_t)k_pool |
+                           (uintptr_t)v_pool) & 15) == 0 &&
+                         ((size_t)num_kv_heads * head_dim * es) % 16 == 0;
+    Kernels ks;
+    if (block_size == kPage && aligned) {
+        if (dtype == LLKV_DTYPE_F32) ks = pick_f32(head_dim, G);
+        else if (dtype == LLKV_DTYPE_F16) ks = pick_fast<_Float16>(head_dim, G);
+        else if (dtype == LLKV_DTYPE_BF16) ks = pick_fast<bf16_t>(head_dim, G);
+    }
+    const int max_pages_hint = (max_seq_len + block_size - 1) / block_size;
+    bool balanced = false;
+    if (num_splits == 0 && ks.split != nullptr) {
+        const AutoChoice c = auto_schedule(ks, num_seqs, num_kv_heads, max_pages_hint);
+        balanced = c.balanced;
+        if (!balanced) num_splits = c.splits;
+    }
 
     DecodeArgs a;
     a.out = out;
@@ -314,59 +577,59 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
     a.v = v_pool;
     a.bt = block_table;
     a.lens = seq_lens;
-    size_t n = (size_t)num_seqs * num_q_heads * p.S_max;
-    char* ws = reinterpret_cast<char*>(workspace);
-    a.part_lse = need ? reinterpret_cast<float*>(ws) : nullptr;
-    a.part_o = need ? reinterpret_cast<float*>(ws + lse_bytes(n)) : nullptr;
     a.B = num_seqs;
     a.Hq = num_q_heads;
     a.Hkv = num_kv_heads;
     a.D = head_dim;
     a.bs = block_size;
     a.max_blocks = max_blocks_per_seq;
-    a.S_max = p.S_max;
-    a.pps_auto = p.pps_auto;
-    a.fixed_S = p.fixed_S;
     a.scale_log2 = scale * kLog2e;
-
-    const int G = num_q_heads / num_kv_heads;
+    a.nwg = 0;
+    a.plan = nullptr;
+    char* ws = reinterpret_cast<char*>(workspace);
     hipStream_t st = (hipStream_t)stream;
-    // The fast kernel needs 16-token pages, 16-byte aligned rows and pointers.
-    const size_t es = dtype_bytes(dtype);
-    const bool aligned = (((uintptr_t)q | (uintptr_t)out | (uintptr_t)k_pool |
-                           (uintptr_t)v_pool) & 15) == 0 &&
-                         ((size_t)num_kv_heads * head_dim * es) % 16 == 0;
-    DecodeFn fast = nullptr;
-    if (block_size == kPage && aligned) {
-        if (dtype == LLKV_DTYPE_F32) fast = pick_f32(head_dim, G);
-        else if (dtype == LLKV_DTYPE_F16) fast = pick_fast<_Float16>(head_dim, G);
-        else if (dtype == LLKV_DTYPE_BF16) fast = pick_fast<bf16_t>(head_dim, G);
-    }
-    if (fast) {
-        dim3 grid(p.S_max, num_kv_heads, num_seqs);
-        fast<<<grid, 64 * kDecodeWaves, 0, st>>>(a);
+
+    if (balanced) {
+        const BalancedWs w = balanced_workspace(num_seqs, num_q_heads, num_kv_heads, head_dim);
+        if (workspace == nullptr || workspace_bytes < w.total)
+            return set_error(LLKV_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn,
+                             workspace_bytes, w.total);
+        a.nwg = balanced_wgs(ks.balanced, (int64_t)num_seqs * num_kv_heads * max_pages_hint);
+        a.plan = reinterpret_cast<int*>(ws + w.plan_off);
+        a.part_lse = reinterpret_cast<float*>(ws + w.lse_off);
+        a.part_o = reinterpret_cast<float*>(ws + w.o_off);
+        a.S_max = 0;
+        a.pps_auto = 0;
+        a.fixed_S = 0;
+        ks.balanced<<<dim3(a.nwg), 64 * kDecodeWaves, 0, st>>>(a);
+        if (int e = check_launch(fn)) return e;
     } else {
-        dim3 grid(p.S_max, num_q_heads, num_seqs);
-        if (dtype == LLKV_DTYPE_F32) decode_generic_kernel<float><<<grid, 64, 0, st>>>(a);
-        else if (dtype == LLKV_DTYPE_F16) decode_generic_kernel<_Float16><<<grid, 64, 0, st>>>(a);
-        else decode_generic_kernel<bf16_t><<<grid, 64, 0, st>>>(a);
-    }
-    if (int e = check_launch(fn)) return e;
-    if (p.S_max > 1) {
-        dim3 grid(num_q_heads, num_seqs);
-        const bool wide = head_dim > 128;
-        if (dtype == LLKV_DTYPE_F32) {
-            if (wide) decode_merge_kernel<float, 4><<<grid, 64, 0, st>>>(a);
-            else decode_merge_kernel<float, 2><<<grid, 64, 0, st>>>(a);
-        } else if (dtype == LLKV_DTYPE_F16) {
-            if (wide) decode_merge_kernel<_Float16, 4><<<grid, 64, 0, st>>>(a);
-            else decode_merge_kernel<_Float16, 2><<<grid, 64, 0, st>>>(a);
+        Plan p = make_plan(block_size, max_seq_len, num_splits);
+        size_t need = fixed_workspace(num_seqs, num_q_heads, head_dim, p);
+        if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+            return set_error(LLKV_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn,
+                             workspace_bytes, need);
+        size_t n = (size_t)num_seqs * num_q_heads * p.S_max;
+        a.part_lse = need ? reinterpret_cast<float*>(ws) : nullptr;
+        a.part_o = need ? reinterpret_cast<float*>(ws + align256(n * sizeof(float))) : nullptr;
+        a.S_max = p.S_max;
+        a.pps_auto = p.pps_auto;
+        a.fixed_S = p.fixed_S;
+        if (ks.split) {
+            dim3 grid(p.S_max, num_kv_heads, num_seqs);
+            ks.split<<<grid, 64 * kDecodeWaves, 0, st>>>(a);
         } else {
-            if (wide) decode_merge_kernel<bf16_t, 4><<<grid, 64, 0, st>>>(a);
-            else decode_merge_kernel<bf16_t, 2><<<grid, 64, 0, st>>>(a);
+            dim3 grid(p.S_max, num_q_heads, num_seqs);
+            if (dtype == LLKV_DTYPE_F32) decode_generic_kernel<float><<<grid, 64, 0, st>>>(a);
+            else if (dtype == LLKV_DTYPE_F16) decode_generic_kernel<_Float16><<<grid, 64, 0, st>>>(a);
+            else decode_generic_kernel<bf16_t><<<grid, 64, 0, st>>>(a);
         }
         if (int e = check_launch(fn)) return e;
+        if (p.S_max <= 1) return LLKV_OK;
     }
-    return LLKV_OK;
+    dim3 grid(num_q_heads, num_seqs);
+    if (dtype == LLKV_DTYPE_F32) launch_merge<float>(balanced, head_dim, grid, st, a);
+    else if (dtype == LLKV_DTYPE_F16) launch_merge<_Float16>(balanced, head_dim, grid, st, a);
+    else launch_merge<bf16_t>(balanced, head_dim, grid, st, a);
+    return check_launch(fn);
 }
-

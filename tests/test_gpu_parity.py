@@ -256,6 +256,48 @@ def test_decode_edge_cases(name, hq, hkv, d, lengths, dtype):
         case.k_pool, case.v_pool = kp.cpu(), vp.cpu()
 
 
+BALANCE = [
+    # (name, lengths, max_seq_len hint (None = true max), dtype)
+    ("sparse_many_empty_wgs", [0, 1, 0, 2, 0], 4096, torch.float32),
+    ("hint_too_small", [600, 33, 1, 257], 1, torch.float32),
+    ("lognormal_200", None, None, torch.float32),
+    ("lognormal_200_fp16", None, None, torch.float16),
+    ("over_balance_limit_1100", "short1100", None, torch.float32),
+    ("all_empty", [0, 0, 0], 64, torch.float32),
+]
+
+
+@pytest.mark.parametrize("name,lengths,hint,dtype", BALANCE, ids=[b[0] for b in BALANCE])
+def test_decode_auto_schedule_shapes(name, lengths, hint, dtype):
+    """num_splits = 0: the balanced schedule (work-groups with empty shares, units cut
+    across many work-groups, wrong length hints) and the fixed fallback past its batch
+    limit."""
+    g = torch.Generator().manual_seed(99)
+    if lengths is None:
+        z = torch.randn(200, generator=g, dtype=torch.float64)
+        lengths = torch.exp(5.5 + z).round().clamp(1, 3000).to(torch.int64).tolist()
+    elif lengths == "short1100":
+        lengths = torch.randint(0, 41, (1100,), generator=g).tolist()
+    say(f"decode auto schedule {name}: B={len(lengths)} max L={max(lengths)} hint={hint} {dtype}")
+    hq, hkv, d = 14, 2, 64
+    need = sum((L + 15) // 16 for L in lengths) + 4
+    case = wl.decode_case(name, len(lengths), hq, hkv, d, lengths, need, dtype, seed=7, append=False,
+                          max_blocks=max(1, max((L + 15) // 16 for L in lengths)))
+    kp, vp = case.k_pool.to(DEV), case.v_pool.to(DEV)
+    max_len = case.max_seq_len if hint is None else hint
+    out = kc.paged_decode(case.q.to(DEV), kp, vp, case.block_table.to(DEV), case.seq_lens.to(DEV),
+                          max_len, num_splits=0, scale=case.scale)
+    torch.cuda.synchronize()
+    ref = oracle_decode(case, np_pool(case.k_pool), np_pool(case.v_pool))
+    if dtype == torch.float32:
+        check_fp32(out, ref, name)
+    else:
+        check_lowp(out, ref, name, 2e-3)
+    for b, L in enumerate(lengths):
+        if L == 0:
+            assert torch.count_nonzero(out[b]).item() == 0
+
+
 def test_decode_noncontiguous_table_and_empty():
     say("decode: table [7,3,11], zero-length sequence in a batch")
     g = torch.Generator().manual_seed(13)
