@@ -1,6 +1,6 @@
 """Benchmark of the paged KV-cache hot path on one MI355X.
 
-Headline (BASELINE.json metric): paged decode at B=64, configuration 2 --
+Headline metric: paged decode at B=64, configuration 2 --
 Qwen2.5-0.5B attention (14 q / 2 kv heads, head_dim 64), fp32, contexts
 U[128, 2048], pool 32768 pages.  One step = one layer of a decode step: KV
 append of the 64 new tokens by slot mapping, then paged decode attention
@@ -8,11 +8,12 @@ over the updated tables.  Steps rotate over --layers independent K/V pools
 (one per layer, as in a model), so the KV bytes of a step are not resident
 in the 256 MB last-level cache from the previous step.
 
-Reported: value = achieved algorithmic HBM GB/s of the decode step (exact
-tokens), us per layer, the decode kernel's roofline fraction (HIP events
-around each decode launch), the CPU baseline (the C oracle = the
-reference's reconstruct_kv + cpu_attention, on this host), and configuration
-4's paged prefill as MFMA utilisation.
+Reported: value = achieved algorithmic HBM GB/s of paged decode (exact
+tokens; HIP events around a HIP-graph replay of --steps decode calls),
+us per layer (graph replay of --steps append + decode steps), the decode
+roofline fraction, the CPU baseline (the C oracle = the reference's
+reconstruct_kv + cpu_attention, on this host), and configuration 4's paged
+prefill as MFMA utilisation.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20]
 
@@ -23,6 +24,10 @@ Profiling helpers (the commands that produce the summaries under profiles/):
   python bench.py --rocprof-summary DIR     per-kernel averages of the rocprofv3
                                             CSV files (kernel trace, counters)
                                             found under DIR
+  python bench.py --rocprof-traffic FETCH_DIR WRITE_DIR CAL_FETCH_DIR CAL_WRITE_DIR
+                                            HBM bytes per decode call from
+                                            FETCH_SIZE / WRITE_SIZE runs of this
+                                            benchmark and of --calibrate-copy
 """
 from __future__ import annotations
 
@@ -90,29 +95,47 @@ def bench_decode(args, torch, kc, wl):
         if ev is not None:
             ev[1].record(stream)
 
+    def decode_only(i):
+        layer = i % L
+        kc.paged_decode(qs[layer], kps[layer], vps[layer], table, lens, max_len, out=outs[layer],
+                        workspace=ws)
+
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+
+    # The timed loops run as HIP graph replays (one launch for K steps), the way a
+    # serving loop issues them: per-call host work (Python, ctypes) is outside.
+    def replay_us(fn, k):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for i in range(k):
+                    fn(i)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        cur = torch.cuda.current_stream()
+        t0.record(cur)
+        graph.replay()
+        t1.record(cur)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) * 1e3 / k
+
+    step_us = replay_us(step, args.steps)
+    dec_us = replay_us(decode_only, args.steps)
+
+    # Eager loop with HIP events around each decode call (host-launch gaps included).
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t0.record(stream)
     for i in range(args.steps):
         step(i, evs[i])
-    t1.record(stream)
     torch.cuda.synchronize()
-    total_ms = t0.elapsed_time(t1)
-    dec_us = [a.elapsed_time(b) * 1e3 for a, b in evs]
-    # the same step without per-launch events (the headline step time)
-    torch.cuda.synchronize()
-    t2, t3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t2.record(stream)
-    for i in range(args.steps):
-        step(i)
-    t3.record(stream)
-    torch.cuda.synchronize()
-    plain_ms = t2.elapsed_time(t3)
+    eager_us = [a_.elapsed_time(b_) * 1e3 for a_, b_ in evs]
 
     # correctness spot check of layer 0 against the oracle (double)
     import numpy as np
@@ -129,9 +152,8 @@ def bench_decode(args, torch, kc, wl):
     dec_bytes_pages = wl.decode_bytes(case, exact_tokens=False)
     app_bytes = wl.append_bytes(case)
     return {
-        "case": case, "host_pools": (ke, ve), "step_ms": plain_ms / args.steps,
-        "step_ms_with_events": total_ms / args.steps,
-        "decode_us_mean": statistics.fmean(dec_us), "decode_us_median": statistics.median(dec_us),
+        "case": case, "host_pools": (ke, ve), "step_ms": step_us / 1e3,
+        "decode_us_mean": dec_us, "decode_us_eager_median": statistics.median(eager_us),
         "decode_bytes": dec_bytes, "decode_bytes_pages": dec_bytes_pages, "append_bytes": app_bytes,
         "parity_ok": ok, "max_abs_err": float(err.max()),
     }
@@ -150,11 +172,20 @@ def bench_prefill(args, torch, kc, wl):
     for _ in range(5):
         run()
     torch.cuda.synchronize()
-    n = max(20, args.steps // 2)
+    n = max(20, args.steps // 4)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(n):
+                run()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    for _ in range(n):
-        run()
+    graph.replay()
     b.record()
     torch.cuda.synchronize()
     us = a.elapsed_time(b) * 1e3 / n
@@ -222,8 +253,12 @@ def rocprof_summary(path: str) -> None:
 
     def short(n):
         if n.startswith("_Z"):
+            # binutils' c++filt predates the _Float16 mangling (DF16_); spell it as
+            # IEEE half (Dh) and rename afterwards
             try:
-                n = subprocess.run(["c++filt", n], capture_output=True, text=True).stdout.strip() or n
+                d = subprocess.run(["c++filt", n.replace("DF16_", "Dh")], capture_output=True,
+                                   text=True).stdout.strip()
+                n = d.replace("half", "_Float16") if d else n
             except OSError:
                 pass
         n = n.replace("(anonymous namespace)::", "")
@@ -247,6 +282,48 @@ def rocprof_summary(path: str) -> None:
         print(f"{'dispatches':>10} {'mean_per_dispatch':>18}  counter  kernel")
         for (n, c), v in sorted(agg.items()):
             print(f"{len(v):10d} {statistics.fmean(v):18.1f}  {c}  {n}")
+
+
+def _counter_means(path: str, counter: str):
+    """{kernel short name: mean counter value per dispatch} from rocprofv3 CSV under path."""
+    import csv
+    import glob
+    import re
+    out = {}
+    for f in glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] != counter:
+                continue
+            n = r["Kernel_Name"].replace("(anonymous namespace)::", "")
+            out.setdefault(re.sub(r"\(.*", "", n).replace("void ", "").strip(), []).append(
+                float(r["Counter_Value"]))
+    return {k: statistics.fmean(v) for k, v in out.items()}
+
+
+def rocprof_traffic(fetch_dir, write_dir, cal_fetch_dir, cal_write_dir) -> None:
+    """Per-call HBM traffic of llkv_paged_decode on configuration 2: FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch) of its kernels, each scaled by bytes / counter of the
+    plain copy of --calibrate-copy."""
+    cf = _counter_means(cal_fetch_dir, "FETCH_SIZE")
+    cw = _counter_means(cal_write_dir, "WRITE_SIZE")
+    copy_f = max((v for k, v in cf.items() if "copyBuffer" in k or "copy" in k.lower()), default=None)
+    copy_w = max((v for k, v in cw.items() if "copyBuffer" in k or "copy" in k.lower()), default=None)
+    f_scale = COPY_CAL_BYTES / copy_f if copy_f else None
+    w_scale = COPY_CAL_BYTES / copy_w if copy_w else None
+    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
+    write = _counter_means(write_dir, "WRITE_SIZE")
+    print(f"copy calibration: {COPY_CAL_BYTES} B read -> FETCH_SIZE {copy_f:.1f}, "
+          f"{COPY_CAL_BYTES} B written -> WRITE_SIZE {copy_w:.1f}")
+    print(f"scale: fetch {f_scale:.3f} B per unit, write {w_scale:.3f} B per unit")
+    total = 0.0
+    for k in sorted(set(fetch) | set(write)):
+        if "decode" not in k:
+            continue
+        fb = fetch.get(k, 0.0) * f_scale
+        wb = write.get(k, 0.0) * w_scale
+        total += fb + wb
+        print(f"{k}: read {fb / 1e6:.3f} MB, written {wb / 1e6:.3f} MB per dispatch")
+    print(f"traffic_bytes_per_call: {total:.0f}")
 
 
 def read_traffic():
@@ -274,9 +351,13 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--rocprof-summary", metavar="DIR")
+    ap.add_argument("--rocprof-traffic", nargs=4, metavar="DIR")
     args = ap.parse_args()
     if args.rocprof_summary:
         rocprof_summary(args.rocprof_summary)
+        return
+    if args.rocprof_traffic:
+        rocprof_traffic(*args.rocprof_traffic)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build's path has no multi-GPU "
@@ -316,14 +397,17 @@ def main():
                    "batch": 64, "layers_rotated": args.layers},
         "us_per_layer": round(step_us, 2),
         "step_GBps_incl_append": round(step_gbs, 1),
-        "decode_kernel_us": round(dec["decode_us_mean"], 2),
+        "decode_us": round(dec["decode_us_mean"], 2),
+        "decode_us_eager_median": round(dec["decode_us_eager_median"], 2),
         "decode_GBps_page_granular": round(dec["decode_bytes_pages"] / (dec["decode_us_mean"] * 1e-6) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "llkv_paged_decode = decode_mfma_f32_kernel<64,7> (split) + "
-                               "decode_merge_kernel<float,1> (split merge)",
+                     "kernel": "llkv_paged_decode (automatic schedule for this batch: "
+                               "decode_split_kernel<MfmaF32Decode<64,7>> S=8, then "
+                               "decode_merge_kernel<float,1>)",
                      "bytes_per_launch": dec["decode_bytes"],
-                     "timing": "HIP events on the launch stream around each llkv_paged_decode call"},
+                     "timing": "HIP events on the launch stream around a HIP-graph replay of "
+                               "--steps llkv_paged_decode calls (4 layer pools rotated)"},
         "parity_ok": dec["parity_ok"],
         "cpu_baseline": cpu,
     }

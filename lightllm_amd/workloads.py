@@ -1,5 +1,5 @@
 """Seeded synthetic inputs for the five configurations of the paged KV-cache path
-(BASELINE.json "configs"), built on the host with torch's CPU generator.
+(the benchmark configurations 1-5), built on the host with torch's CPU generator.
 
 Each builder returns plain host tensors (pools [num_blocks, 16, Hkv, D], int32
 block tables padded with -1, int32 lengths, int64 slot mappings), so tests and

@@ -6,7 +6,8 @@ file:line each function follows).  Only tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg import this module, and only as the checker or
 the CPU baseline; the product library never calls it.
 
-Pinning (what each function is checked against) is listed in oracle/README.md.
+Pinning (what each function is checked against) is listed in oracle/cpu_ref.h;
+no function is left unpinned.
 """
 from __future__ import annotations
 

@@ -11,7 +11,29 @@
  *     K, V : [num_blocks, block_size, Hkv, D]   row-major
  *     slot = phys * block_size + pos % block_size,  phys = table[pos / block_size]
  *
- * Pinning status of each function is listed in oracle/README.md.
+ *
+ * Pinning (what each function is checked against, tests/test_oracle.py unless noted):
+ *   llo_fill_random, llo_rng_randf_fill   closed-form LCG known answers
+ *   llo_f32_to_f16 / llo_f16_to_f32       numpy float16 casts (RNE, subnormals, ties, overflow)
+ *   llo_f32_to_bf16 / llo_bf16_to_f32     torch bfloat16 casts (RNE, ties)
+ *   llo_append_slots, llo_scatter_prefill, llo_scatter_prefill_batched, llo_reconstruct_kv
+ *                                         numpy fancy indexing of the pool, bit-exact;
+ *                                         append-then-gather identity
+ *   llo_cpu_attention[_f64], llo_paged_decode[_f64]
+ *                                         numpy float64 softmax attention; closed forms
+ *                                         (one key -> V[0], equal keys -> mean V, length 0
+ *                                         -> zeros); convex hull; the reference's ramp
+ *                                         known-answer inputs (tests/test_paged_attention.cu:69-130)
+ *   llo_splitk_partials, llo_splitk_merge unsplit result for S in {1,2,4,16,40}; a hand-built
+ *                                         two-split + identity-split merge
+ *   llo_prefill_attention[_f64], llo_prefill_attention_test_causal
+ *                                         numpy masked softmax; pure-Python brute force on
+ *                                         P <= 4, L <= 48; test-file causal form equals the
+ *                                         kernel form when total = hist + P
+ *   llo_paged_prefill[_f64]               numpy per-sequence gather + masked softmax
+ *   llo_first_prefill_batched             numpy per-entry causal softmax
+ *   llo_fnv1a_tokens                      published FNV-1a 64 vectors ("", "a", "abc")
+ * No function is left unpinned.
  */
 #ifndef LIGHTLLM_ORACLE_CPU_REF_H
 #define LIGHTLLM_ORACLE_CPU_REF_H

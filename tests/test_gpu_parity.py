@@ -1,10 +1,10 @@
 """Parity of the gfx950 kernels (through the C ABI) against the CPU oracle.
 
-Bars:
+Bars (the path's parity contract):
   * append / scatter / gather: bit-exact (compared as raw bits);
   * fp32 attention: |gpu - ref| <= 1e-6 + 1e-5 |ref|, ref = the oracle carried in
     double (the fp32 oracle's own rounding is of the same order, so the double
-    result is the judge, as the survey's oracle plan states);
+    result is the judge);
   * fp16 KV: |gpu - ref| <= 2e-3 (|ref| + rms_D(ref)), ref = double-precision
     oracle on the fp16 values, rms_D = RMS of that output vector over head_dim
     (the relative bar taken against the vector's magnitude, so components near
