@@ -15,7 +15,7 @@
 ///    (as the reference does, :555-560, :1036-1037) to size the launch; the
 ///    C ABI takes host-side bounds instead and never synchronises.
 /// Extensions (new, additive): append_kv_slots (slot-mapping append),
-/// paged_prefill_varlen (N sequences in one launch), gather_kv.
+/// paged_prefill_varlen (N sequences in one launch).
 
 #include <cstdint>
 

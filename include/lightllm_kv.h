@@ -147,14 +147,22 @@ int llkv_paged_decode(void* out, const void* q, const void* k_pool,
  *             attends keys at positions <= its own (self included), as the
  *             reference kernel (src/kv_cache/paged_attention.cu:658,712).
  * max_q_len, max_seq_len: host-side upper bounds (grid sizing).
+ * workspace : device memory of llkv_paged_prefill_workspace_size() bytes for
+ *             the fp32 partials of long key ranges, which are then cut into
+ *             chunks run in parallel; NULL (or a size of 0) runs every key
+ *             range unsplit.  Calls sharing one workspace must not overlap.
  * ------------------------------------------------------------------------ */
+size_t llkv_paged_prefill_workspace_size(int num_seqs, int total_q, int max_q_len,
+                                         int max_seq_len, int num_q_heads,
+                                         int head_dim, int block_size, int dtype);
 int llkv_paged_prefill(void* out, const void* q, const void* k_pool,
                        const void* v_pool, const int* block_table,
                        int max_blocks_per_seq, const int* cu_q,
                        const int* seq_lens, int num_seqs, int total_q,
                        int max_q_len, int max_seq_len, int num_q_heads,
                        int num_kv_heads, int head_dim, int block_size,
-                       int causal, float scale, int dtype, void* stream);
+                       int causal, float scale, int dtype, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* Replaces first_prefill_attn_batched_gpu[_dispatch]
  * (include/lightllm/kv_cache/paged_attention.h:130-145,

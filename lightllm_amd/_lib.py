@@ -44,9 +44,11 @@ _SIGS = {
     "llkv_paged_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                   c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int,
                                   c_void_p, c_size_t, c_void_p]),
+    "llkv_paged_prefill_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                                     c_int]),
     "llkv_paged_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
                                    c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
-                                   c_int, c_float, c_int, c_void_p]),
+                                   c_int, c_float, c_int, c_void_p, c_size_t, c_void_p]),
     "llkv_first_prefill_batched": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                            c_int, c_int, c_float, c_int, c_void_p]),

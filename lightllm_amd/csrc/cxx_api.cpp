@@ -42,7 +42,7 @@ struct Scratch {
         ptr = nullptr;
         bytes = 0;
         hip_throw(hipMalloc(&ptr, need), "hipMalloc(workspace)");
-        hip_throw(hipMemset(ptr, 0, need), "hipMemset(workspace)");   // counters start at zero
+        hip_throw(hipMemset(ptr, 0, need), "hipMemset(workspace)");
         bytes = need;
         return ptr;
     }
@@ -101,11 +101,15 @@ Tensor paged_prefill_varlen(const Tensor& q, const int* block_table, int max_blo
     require_device_pool(allocator, "prefill_paged_attention");
     Tensor out({Ptot, Hq, D}, q.dtype(), Device::CUDA);
     if (Ptot == 0) return out;
+    const size_t ws_bytes = llkv_paged_prefill_workspace_size(num_seqs, Ptot, max_q_len, max_seq_len, Hq,
+                                                              D, allocator.block_size(),
+                                                              static_cast<int>(q.dtype()));
+    void* ws = ws_bytes ? t_workspace.get(ws_bytes) : nullptr;
     throw_if(llkv_paged_prefill(out.raw(), q.raw(), allocator.k_storage_raw(), allocator.v_storage_raw(),
                                 block_table, max_blocks, cu_q, seq_lens, num_seqs, Ptot, max_q_len,
                                 max_seq_len, Hq, allocator.num_kv_heads(), D, allocator.block_size(),
                                 causal ? 1 : 0, 1.0f / std::sqrt((float)D),
-                                static_cast<int>(q.dtype()), nullptr),
+                                static_cast<int>(q.dtype()), ws, ws_bytes, nullptr),
              "prefill_paged_attention");
     return out;
 }

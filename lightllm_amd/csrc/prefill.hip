@@ -159,13 +159,21 @@ int launch_rows(const RowArgs& a, int rows, int dtype, hipStream_t st) {
 
 using namespace llkv;
 
+extern "C" size_t llkv_paged_prefill_workspace_size(int num_seqs, int total_q, int max_q_len,
+                                                    int max_seq_len, int num_q_heads,
+                                                    int head_dim, int block_size, int dtype) {
+    return prefill_mfma_workspace(num_seqs, num_q_heads, head_dim, block_size, dtype, total_q,
+                                  max_q_len, max_seq_len);
+}
+
 extern "C" int llkv_paged_prefill(void* out, const void* q, const void* k_pool,
                                   const void* v_pool, const int* block_table,
                                   int max_blocks_per_seq, const int* cu_q,
                                   const int* seq_lens, int num_seqs, int total_q,
                                   int max_q_len, int max_seq_len, int num_q_heads,
                                   int num_kv_heads, int head_dim, int block_size,
-                                  int causal, float scale, int dtype, void* stream) {
+                                  int causal, float scale, int dtype, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
     const char* fn = "llkv_paged_prefill";
     if (num_seqs == 0 || total_q == 0) return LLKV_OK;
     if (num_seqs < 0 || total_q < 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
@@ -196,7 +204,7 @@ extern "C" int llkv_paged_prefill(void* out, const void* q, const void* k_pool,
     m.causal = causal;
     m.scale_log2 = scale * kLog2e;
     int r = launch_prefill_mfma(m, head_dim, block_size, dtype, total_q, max_q_len,
-                                max_seq_len, st);
+                                max_seq_len, workspace, workspace_bytes, st);
     if (r != -1) return r;   // -1: shape not covered by the MFMA kernel
 
     RowArgs a = {};

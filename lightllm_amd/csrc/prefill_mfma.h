@@ -18,6 +18,11 @@
 //                 B = P^T from registers.
 // Causal masking uses the reference's rule: query i of a P-row chunk over L
 // keys sits at L - P + i and sees keys <= that position.
+//
+// Long key ranges are cut into chunks of kChunkTiles tiles, one work-group
+// each (grid: (N x qblocks x max_chunks, Hq)), so that a cached prefix of
+// thousands of keys does not serialise on one work-group; their fp32 partials
+// (normalised rows + log2-sum-exp2) are merged by prefill_merge_kernel.
 #pragma once
 
 #include "attn_common.h"
@@ -34,11 +39,21 @@ struct MfmaPrefillArgs {
     const int* lens;
     int max_blocks, N, Hq, Hkv, causal;
     float scale_log2;
-    int qblocks;   // query blocks per sequence (grid.x = N * qblocks)
+    int qblocks;      // query blocks per sequence
+    int max_chunks;   // key chunks per (sequence, query block); grid.x = N * qblocks * max_chunks
+    int chunk_tiles;  // key tiles per chunk
+    float* part_o;    // [N*qblocks*max_chunks*Hq][BQ][D] (max_chunks > 1)
+    float* part_lse;  // [N*qblocks*max_chunks*Hq][BQ]
 };
 
+// Workspace bytes for the chunked schedule (0: the shape runs unchunked).
+size_t prefill_mfma_workspace(int N, int Hq, int head_dim, int block_size, int dtype,
+                              int total_q, int max_q_len, int max_seq_len);
+
 // Returns -1 when the shape is not handled (caller falls back), else a status.
+// workspace may be NULL (then no key range is split).
 int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dtype,
-                        int total_q, int max_q_len, int max_seq_len, hipStream_t st);
+                        int total_q, int max_q_len, int max_seq_len, void* workspace,
+                        size_t workspace_bytes, hipStream_t st);
 
 }  // namespace llkv

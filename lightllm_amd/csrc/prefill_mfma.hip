@@ -12,6 +12,9 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// Native vector for staged K/V rows (HIP's uint4 struct is copied with memcpy,
+// which keeps the staging registers in scratch memory).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T> struct Mfma;
 
@@ -41,8 +44,8 @@ template <int D>
 struct Smem {
     static constexpr int KPAD = D + 8;    // halves per K row (pad: spread LDS banks)
     static constexpr int VPAD = BN + 8;   // halves per V^T row
-    uint16_t k[2][BN * KPAD];
-    uint16_t vt[2][D * VPAD];
+    alignas(16) uint16_t k[2][BN * KPAD];
+    alignas(16) uint16_t vt[2][D * VPAD];
     int pages[1024];   // page ids [tbase, tbase + 1024) of the sequence
 };
 
@@ -61,8 +64,10 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const int g = lane >> 4, c16 = lane & 15;
     const int hq = blockIdx.y;
     const int kvh = hq / (a.Hq / a.Hkv);
-    const int n = blockIdx.x / a.qblocks;
-    const int qb = a.qblocks - 1 - (blockIdx.x % a.qblocks);   // heavy (late) blocks first
+    const int unit = blockIdx.x / a.max_chunks;        // (sequence, query block)
+    const int ci = blockIdx.x - unit * a.max_chunks;   // key chunk of the unit
+    const int n = unit / a.qblocks;
+    const int qb = a.qblocks - 1 - (unit % a.qblocks);   // heavy (late) blocks first
 
     const int q0 = a.cu_q[n];
     const int P = a.cu_q[n + 1] - q0;
@@ -74,6 +79,11 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     int kend = a.causal ? L - P + min(q_lo + BQ, P) : L;
     kend = kend < 0 ? 0 : (kend > L ? L : kend);
     const int ntiles = (kend + BN - 1) / BN;
+    const int nchunks = (ntiles + a.chunk_tiles - 1) / a.chunk_tiles;
+    if (ci > 0 && ci >= nchunks) return;   // chunk 0 also covers an empty key range (zeros)
+    const int t_begin = ci * a.chunk_tiles;
+    const int t_end = min(t_begin + a.chunk_tiles, ntiles);
+    const bool direct = nchunks <= 1;
     const int last_page = L > 0 ? (L - 1) / kPage : 0;
     const int* bt = a.bt + (int64_t)n * a.max_blocks;
     const int64_t row_elems = (int64_t)a.Hkv * D;
@@ -104,6 +114,11 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         qpos[nt] = ql < P ? (a.causal ? L - P + ql : L - 1) : -1;
     }
 
+    // Smallest query position of the wave's 32 rows (every row valid), for the
+    // unmasked fast path of tiles that lie entirely below it.
+    const int wq0 = q_lo + w * WQ;
+    const int wave_min_pos = (wq0 + WQ <= P) ? (a.causal ? L - P + wq0 : L - 1) : -1;
+
     f32x4 o[DT][2];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -114,9 +129,9 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 
     // ---- staging: global -> registers -> LDS -----------------------------
     int tbase = 0;   // first page id held in sm.pages
-    uint4 kreg[KCH_T];
-    uint4 vreg[VT_T][2];
-    auto load_tile = [&](int t) {
+    u32x4 kr[KCH_T];
+    u32x4 vr[VT_T][2];
+    auto load_tile = [&](int t, u32x4 (&kreg)[KCH_T], u32x4 (&vreg)[VT_T][2]) {
         const int key0 = t * BN;
 #pragma unroll
         for (int j = 0; j < KCH_T; ++j) {
@@ -124,7 +139,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             const int key = ch / (D / 8), c = ch % (D / 8);
             const int page = min((key0 + key) >> 4, last_page);
             const int64_t row = (int64_t)max(sm.pages[page - tbase], 0) * kPage + ((key0 + key) & 15);
-            kreg[j] = *reinterpret_cast<const uint4*>(kg + row * row_elems + c * 8);
+            kreg[j] = *reinterpret_cast<const u32x4*>(kg + row * row_elems + c * 8);
         }
 #pragma unroll
         for (int j = 0; j < VT_T; ++j) {
@@ -133,29 +148,30 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             const int key = key0 + 2 * kp;
             const int page = min(key >> 4, last_page);
             const int64_t row = (int64_t)max(sm.pages[page - tbase], 0) * kPage + (key & 15);
-            vreg[j][0] = *reinterpret_cast<const uint4*>(vg + row * row_elems + c * 8);
-            vreg[j][1] = *reinterpret_cast<const uint4*>(vg + (row + 1) * row_elems + c * 8);
+            vreg[j][0] = *reinterpret_cast<const u32x4*>(vg + row * row_elems + c * 8);
+            vreg[j][1] = *reinterpret_cast<const u32x4*>(vg + (row + 1) * row_elems + c * 8);
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](int buf, const u32x4 (&kreg)[KCH_T], const u32x4 (&vreg)[VT_T][2]) {
 #pragma unroll
         for (int j = 0; j < KCH_T; ++j) {
             const int ch = tid + 256 * j;
             const int key = ch / (D / 8), c = ch % (D / 8);
-            *reinterpret_cast<uint4*>(&sm.k[buf][key * KPAD + c * 8]) = kreg[j];
+            *reinterpret_cast<u32x4*>(&sm.k[buf][key * KPAD + c * 8]) = kreg[j];
         }
 #pragma unroll
         for (int j = 0; j < VT_T; ++j) {
             const int task = tid + 256 * j;
             const int kp = task % (BN / 2), c = task / (BN / 2);
-            const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&vreg[j][0]);
-            const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&vreg[j][1]);
+            // keys 2kp (v0) and 2kp+1 (v1), dims 8c..8c+7: dim e's pair (v0[e], v1[e]) is one
+            // dword of V^T, built with v_perm_b32 (low halves: 0x05040100, high: 0x07060302)
+            const uint32_t a0[4] = {vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w};
+            const uint32_t a1[4] = {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w};
+            uint32_t* dst = reinterpret_cast<uint32_t*>(&sm.vt[buf][(c * 8) * VPAD + 2 * kp]);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t lo = (v0[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-                const uint32_t hi = (v1[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-                *reinterpret_cast<uint32_t*>(&sm.vt[buf][(c * 8 + e) * VPAD + 2 * kp]) =
-                    lo | (hi << 16);
+            for (int e2 = 0; e2 < 4; ++e2) {
+                dst[(2 * e2) * (VPAD / 2)] = __builtin_amdgcn_perm(a1[e2], a0[e2], 0x05040100u);
+                dst[(2 * e2 + 1) * (VPAD / 2)] = __builtin_amdgcn_perm(a1[e2], a0[e2], 0x07060302u);
             }
         }
     };
@@ -166,20 +182,20 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         for (int i = tid; i < 1024; i += 256) sm.pages[i] = bt[min(base + i, last_page)];
         __syncthreads();
     };
-    if (ntiles > 0) {
-        stage_pages(0);
-        load_tile(0);
-        store_tile(0);
+    if (t_begin < t_end) {
+        stage_pages(4 * t_begin);
+        load_tile(t_begin, kr, vr);
+        store_tile(0, kr, vr);
     }
     __syncthreads();
 
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < ntiles) {
+    for (int t = t_begin; t < t_end; ++t) {
+        const int buf = (t - t_begin) & 1;
+        if (t + 1 < t_end) {
             // tile t+1 covers pages [4(t+1), 4(t+1)+4); restage when they leave the window
             // (uniform branch; every earlier read of sm.pages preceded the last barrier)
             if (4 * (t + 1) + 4 > tbase + 1024) stage_pages(4 * (t + 1));
-            load_tile(t + 1);
+            load_tile(t + 1, kr, vr);
         }
         __builtin_amdgcn_sched_barrier(0);   // next tile's loads issue before this tile's MFMAs
 
@@ -201,41 +217,64 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             }
         }
 
-        // ---- scale, mask, online softmax (per query column) ---------------
+        // ---- mask, online softmax (per query column) ----------------------
+        // Scores stay raw (unscaled) until the exponent: p = 2^(s c - m) with
+        // c = scale * log2(e) > 0, so the row maximum commutes with the scaling.
         const int key0 = t * BN;
+        const float c = a.scale_log2;
+        // Every key of the tile visible to every row of the wave (uniform): no mask.
+        const bool unmasked = key0 + BN - 1 <= wave_min_pos && key0 + BN <= kend;
+        float mx[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            if (!unmasked) {
+                // key = key0 + 8g + (32 ss + 4 h + i) is visible iff key <= min(qpos, kend - 1)
+                const int r = min(qpos[nt], kend - 1) - key0 - 8 * g;
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (32 * (kt >> 1) + 4 * (kt & 1) + i > r) s[kt][nt][i] = -INFINITY;
+            }
+            float v = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v = fmaxf(v, s[kt][nt][i]);
+            v = fmaxf(v, __shfl_xor(v, 16, 64));
+            v = fmaxf(v, __shfl_xor(v, 32, 64));
+            mx[nt] = v * c;
+        }
+        // Lazy rescaling: the running max m only moves when a row's tile max
+        // exceeds it by more than 8 (so p <= 2^8 otherwise); then the whole wave
+        // rescales its accumulators once.  Usually only the first tile does.
+        bool grow = false;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) grow |= mx[nt] > m[nt] + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const float mnew = fmaxf(m[nt], mx[nt]);
+                const float corr = fast_exp2(m[nt] - mnew);
+                m[nt] = mnew;
+                lsum[nt] *= corr;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= corr;
+            }
+        }
         uint4 pop[2][2];   // P^T operands [k-step][query tile]
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            float mx = kNegBig;
-            float sv[4][4];
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                const int ss = kt >> 1, h = kt & 1;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int key = key0 + 32 * ss + 8 * g + 4 * h + i;
-                    const float x = s[kt][nt][i] * a.scale_log2;
-                    sv[kt][i] = (key <= qpos[nt] && key < kend) ? x : -INFINITY;
-                    mx = fmaxf(mx, sv[kt][i]);
-                }
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mnew = fmaxf(m[nt], mx);
-            const float corr = fast_exp2(m[nt] - mnew);
-            m[nt] = mnew;
             float ps = 0.f;
             float pv[4][4];
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    pv[kt][i] = fast_exp2(sv[kt][i] - mnew);
+                    pv[kt][i] = fast_exp2(fmaf(s[kt][nt][i], c, -m[nt]));
                     ps += pv[kt][i];
                 }
-            lsum[nt] = lsum[nt] * corr + ps;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= corr;
+            lsum[nt] += ps;
 #pragma unroll
             for (int ss = 0; ss < 2; ++ss) {
                 pop[ss][nt].x = Mfma<T>::pack2(pv[2 * ss][0], pv[2 * ss][1]);
@@ -257,49 +296,202 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             }
         }
 
-        if (t + 1 < ntiles) store_tile(buf ^ 1);
+        if (t + 1 < t_end) store_tile(buf ^ 1, kr, vr);
         __syncthreads();
     }
 
     // ---- normalise and write: lane holds dims dt*16 + 4g + i of its query --
+    // (one chunk: the output row; several: an fp32 partial row + log2-sum-exp2,
+    // -inf for a row that saw no key of this chunk)
     T* og = reinterpret_cast<T*>(a.out);
+    const int64_t pidx = ((int64_t)unit * a.max_chunks + ci) * a.Hq + hq;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         float lt = lsum[nt];
         lt += __shfl_xor(lt, 16, 64);
         lt += __shfl_xor(lt, 32, 64);
-        const int ql = q_lo + w * WQ + nt * 16 + c16;
+        const int row = w * WQ + nt * 16 + c16;
+        const int ql = q_lo + row;
         if (ql >= P) continue;
         const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-        T* orow = og + ((int64_t)(q0 + ql) * a.Hq + hq) * D;
+        if (direct) {
+            T* orow = og + ((int64_t)(q0 + ql) * a.Hq + hq) * D;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            uint2 w2;
-            w2.x = Mfma<T>::pack2(o[dt][nt][0] * inv, o[dt][nt][1] * inv);
-            w2.y = Mfma<T>::pack2(o[dt][nt][2] * inv, o[dt][nt][3] * inv);
-            *reinterpret_cast<uint2*>(orow + dt * 16 + 4 * g) = w2;
+            for (int dt = 0; dt < DT; ++dt) {
+                uint2 w2;
+                w2.x = Mfma<T>::pack2(o[dt][nt][0] * inv, o[dt][nt][1] * inv);
+                w2.y = Mfma<T>::pack2(o[dt][nt][2] * inv, o[dt][nt][3] * inv);
+                *reinterpret_cast<uint2*>(orow + dt * 16 + 4 * g) = w2;
+            }
+        } else {
+            float* prow = a.part_o + (pidx * BQ + row) * D;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                *reinterpret_cast<float4*>(prow + dt * 16 + 4 * g) =
+                    make_float4(o[dt][nt][0] * inv, o[dt][nt][1] * inv, o[dt][nt][2] * inv,
+                                o[dt][nt][3] * inv);
+            if (g == 0) a.part_lse[pidx * BQ + row] = lt > 0.f ? m[nt] + fast_log2(lt) : -INFINITY;
         }
     }
 }
 
+// Merge of a (sequence, query block, q head) unit's key chunks: grid
+// (N x qblocks, Hq, BQ / kMergeRows), 4 waves per work-group, kMergeRows / 4
+// rows per wave, lane d holding dims d, d + 64, ...  The loads of all the
+// wave's rows for kMergeBatch chunks are issued together; the log-sum-exp
+// weights are updated online per batch.
+constexpr int kMergeRows = 16;
+constexpr int kMergeBatch = 8;
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
+    constexpr int MD = D / 64;
+    constexpr int RPW = kMergeRows / 4;   // rows per wave
+    const int unit = blockIdx.x, hq = blockIdx.y;
+    const int n = unit / a.qblocks;
+    const int qb = a.qblocks - 1 - (unit % a.qblocks);
+    const int q0 = a.cu_q[n];
+    const int P = a.cu_q[n + 1] - q0;
+    const int q_lo = qb * BQ;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int row0 = blockIdx.z * kMergeRows + w * RPW;
+    if (q_lo + row0 >= P) return;
+    int L = a.lens[n];
+    const int cap = a.max_blocks * kPage;
+    L = L < 0 ? 0 : (L > cap ? cap : L);
+    int kend = a.causal ? L - P + min(q_lo + BQ, P) : L;
+    kend = kend < 0 ? 0 : (kend > L ? L : kend);
+    const int ntiles = (kend + BN - 1) / BN;
+    const int nchunks = (ntiles + a.chunk_tiles - 1) / a.chunk_tiles;
+    if (nchunks <= 1) return;   // written directly
+    const int64_t p0 = ((int64_t)unit * a.max_chunks) * a.Hq + hq;   // chunk c at p0 + c * Hq
+    const int nrows = min(RPW, P - q_lo - row0);
+    float M[RPW], W[RPW], acc[RPW][MD];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        M[r] = -INFINITY;
+        W[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MD; ++i) acc[r][i] = 0.0f;
+    }
+    for (int c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
+        float lv[RPW][kMergeBatch], pv[RPW][kMergeBatch][MD];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                const bool ok = r < nrows && c0 + j < nchunks;
+                const int64_t pc = (p0 + (int64_t)(c0 + j) * a.Hq) * BQ + row0 + r;
+                lv[r][j] = ok ? a.part_lse[pc] : -INFINITY;
+#pragma unroll
+                for (int i = 0; i < MD; ++i) pv[r][j][i] = ok ? a.part_o[pc * D + lane + 64 * i] : 0.0f;
+            }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            float mb = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) mb = fmaxf(mb, lv[r][j]);
+            const float Mn = fmaxf(M[r], mb);
+            if (Mn == -INFINITY) continue;   // no key seen by this row yet
+            const float sc = fast_exp2(M[r] - Mn);
+            W[r] *= sc;
+#pragma unroll
+            for (int i = 0; i < MD; ++i) acc[r][i] *= sc;
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                const float wt = fast_exp2(lv[r][j] - Mn);
+                W[r] += wt;
+#pragma unroll
+                for (int i = 0; i < MD; ++i) acc[r][i] = fmaf(wt, pv[r][j][i], acc[r][i]);
+            }
+            M[r] = Mn;
+        }
+    }
+    T* og = reinterpret_cast<T*>(a.out);
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        if (r >= nrows) break;
+        const float inv = W[r] > 0.f ? 1.0f / W[r] : 0.f;
+        T* orow = og + ((int64_t)(q0 + q_lo + row0 + r) * a.Hq + hq) * D;
+#pragma unroll
+        for (int i = 0; i < MD; ++i) orow[lane + 64 * i] = Elem<T>::from_f32(acc[r][i] * inv);
+    }
+}
+
+bool prefill_mfma_handles(int head_dim, int block_size, int dtype) {
+    return block_size == kPage && (dtype == LLKV_DTYPE_F16 || dtype == LLKV_DTYPE_BF16) &&
+           (head_dim == 64 || head_dim == 128);
+}
+
+// Key tiles per chunk: 16 tiles (1024 keys) keeps a work-group's run short
+// against the 256 CUs while a chunk's K/V traffic stays large against its
+// partial rows.
+constexpr int kChunkTiles = 16;
+
+struct ChunkPlan {
+    int qblocks, max_chunks;
+};
+
+ChunkPlan chunk_plan(int total_q, int max_q_len, int max_seq_len) {
+    ChunkPlan c;
+    const int qmax = (max_q_len > 0 && max_q_len < total_q) ? max_q_len : total_q;
+    c.qblocks = (qmax + BQ - 1) / BQ;
+    const int max_tiles = (std::max(max_seq_len, 1) + BN - 1) / BN;
+    c.max_chunks = std::max(1, (max_tiles + kChunkTiles - 1) / kChunkTiles);
+    return c;
+}
+
 }  // namespace
 
+size_t prefill_mfma_workspace(int N, int Hq, int head_dim, int block_size, int dtype, int total_q,
+                              int max_q_len, int max_seq_len) {
+    if (!prefill_mfma_handles(head_dim, block_size, dtype) || N <= 0 || total_q <= 0) return 0;
+    const ChunkPlan c = chunk_plan(total_q, max_q_len, max_seq_len);
+    if (c.max_chunks <= 1) return 0;
+    const size_t parts = (size_t)N * c.qblocks * c.max_chunks * Hq;
+    return parts * BQ * sizeof(float) + parts * BQ * head_dim * sizeof(float);
+}
+
 int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dtype,
-                        int total_q, int max_q_len, int max_seq_len, hipStream_t st) {
-    (void)max_seq_len;
-    if (block_size != kPage) return -1;
-    if (dtype != LLKV_DTYPE_F16 && dtype != LLKV_DTYPE_BF16) return -1;
-    if (head_dim != 64 && head_dim != 128) return -1;
+                        int total_q, int max_q_len, int max_seq_len, void* workspace,
+                        size_t workspace_bytes, hipStream_t st) {
+    if (!prefill_mfma_handles(head_dim, block_size, dtype)) return -1;
     if (((uintptr_t)a.q | (uintptr_t)a.out | (uintptr_t)a.k | (uintptr_t)a.v) & 15) return -1;
-    int qmax = (max_q_len > 0 && max_q_len < total_q) ? max_q_len : total_q;
-    a.qblocks = (qmax + BQ - 1) / BQ;
-    dim3 grid(a.N * a.qblocks, a.Hq);
+    const ChunkPlan c = chunk_plan(total_q, max_q_len, max_seq_len);
+    a.qblocks = c.qblocks;
+    const size_t need = prefill_mfma_workspace(a.N, a.Hq, head_dim, block_size, dtype, total_q,
+                                               max_q_len, max_seq_len);
+    if (need > 0 && workspace != nullptr && workspace_bytes >= need) {
+        const size_t parts = (size_t)a.N * c.qblocks * c.max_chunks * a.Hq;
+        a.max_chunks = c.max_chunks;
+        a.chunk_tiles = kChunkTiles;
+        a.part_lse = reinterpret_cast<float*>(workspace);
+        a.part_o = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + parts * BQ * sizeof(float));
+    } else {   // no (or too small a) workspace: one chunk per unit
+        a.max_chunks = 1;
+        a.chunk_tiles = 1 << 30;
+        a.part_lse = nullptr;
+        a.part_o = nullptr;
+    }
+    dim3 grid(a.N * a.qblocks * a.max_chunks, a.Hq);
+    dim3 mgrid(a.N * a.qblocks, a.Hq, BQ / kMergeRows);
+    const bool merge = a.max_chunks > 1;
     if (dtype == LLKV_DTYPE_F16) {
-        if (head_dim == 64) prefill_mfma_kernel<_Float16, 64><<<grid, 256, 0, st>>>(a);
-        else prefill_mfma_kernel<_Float16, 128><<<grid, 256, 0, st>>>(a);
+        if (head_dim == 64) {
+            prefill_mfma_kernel<_Float16, 64><<<grid, 256, 0, st>>>(a);
+            if (merge) prefill_merge_kernel<_Float16, 64><<<mgrid, 256, 0, st>>>(a);
+        } else {
+            prefill_mfma_kernel<_Float16, 128><<<grid, 256, 0, st>>>(a);
+            if (merge) prefill_merge_kernel<_Float16, 128><<<mgrid, 256, 0, st>>>(a);
+        }
     } else {
-        if (head_dim == 64) prefill_mfma_kernel<bf16_t, 64><<<grid, 256, 0, st>>>(a);
-        else prefill_mfma_kernel<bf16_t, 128><<<grid, 256, 0, st>>>(a);
+        if (head_dim == 64) {
+            prefill_mfma_kernel<bf16_t, 64><<<grid, 256, 0, st>>>(a);
+            if (merge) prefill_merge_kernel<bf16_t, 64><<<mgrid, 256, 0, st>>>(a);
+        } else {
+            prefill_mfma_kernel<bf16_t, 128><<<grid, 256, 0, st>>>(a);
+            if (merge) prefill_merge_kernel<bf16_t, 128><<<mgrid, 256, 0, st>>>(a);
+        }
     }
     return check_launch("llkv_paged_prefill");
 }

@@ -209,8 +209,8 @@ _WS: dict = {}
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
-    """Decode workspace (split partials), cached per device and grown on demand.  Calls
-    that share it must be ordered on one stream."""
+    """Workspace for the split partials of decode and prefill, cached per device and grown
+    on demand.  Calls that share it must be ordered on one stream."""
     key = str(device)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
@@ -259,8 +259,10 @@ def paged_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                   block_table: torch.Tensor, cu_q: torch.Tensor, seq_lens: torch.Tensor,
                   max_q_len: int, max_seq_len: int, causal: bool = True,
                   scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                  stream=None) -> torch.Tensor:
-    """Varlen paged prefill: q [total_q, Hq, D], sequence n owns rows cu_q[n]:cu_q[n+1]."""
+                  stream=None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Varlen paged prefill: q [total_q, Hq, D], sequence n owns rows cu_q[n]:cu_q[n+1].
+    workspace: uint8 device buffer for the key-chunk partials (default: a cached one);
+    pass an empty tensor to run every key range unsplit."""
     _require(q, k_pool.dtype, "q")
     for name, t in (("block_table", block_table), ("cu_q", cu_q), ("seq_lens", seq_lens)):
         _require(t, torch.int32, name)
@@ -270,10 +272,18 @@ def paged_prefill(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
         scale = 1.0 / math.sqrt(d)
     if out is None:
         out = torch.empty_like(q)
+    n = seq_lens.shape[0]
+    ws_bytes = lib().llkv_paged_prefill_workspace_size(n, tq, max_q_len, max_seq_len, hq, d, bs,
+                                                       dtype_code(q.dtype))
+    if workspace is None and ws_bytes:
+        workspace = _workspace(ws_bytes, q.device)
+    ws_ptr = _ptr(workspace) if workspace is not None else None
+    ws_len = workspace.numel() if workspace is not None else 0
     check(lib().llkv_paged_prefill(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_table),
                                    block_table.shape[1], _ptr(cu_q), _ptr(seq_lens),
-                                   seq_lens.shape[0], tq, max_q_len, max_seq_len, hq, hkv, d, bs,
-                                   1 if causal else 0, scale, dtype_code(q.dtype), _stream(stream)))
+                                   n, tq, max_q_len, max_seq_len, hq, hkv, d, bs,
+                                   1 if causal else 0, scale, dtype_code(q.dtype), ws_ptr, ws_len,
+                                   _stream(stream)))
     return out
 
 

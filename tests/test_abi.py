@@ -40,7 +40,7 @@ def test_python_bindings_cover_the_header():
 
 def test_version_and_status_strings():
     lib = L.lib()
-    assert lib.llkv_abi_version() >= 1
+    assert lib.llkv_abi_version() == 2
     assert L.status_string(0) == "ok"
     assert "invalid" in L.status_string(1)
     assert "unsupported" in L.status_string(2) or "support" in L.status_string(2)
@@ -101,8 +101,20 @@ def test_decode_rejects_small_workspace():
 def test_prefill_argument_checks():
     lib = L.lib()
     rc, msg = _err(lib.llkv_paged_prefill(None, None, None, None, None, 8, None, None, 1, 16, 16,
-                                          16, 14, 2, 512, 16, 1, 0.1, 0, None))
+                                          16, 14, 2, 512, 16, 1, 0.1, 0, None, 0, None))
     assert rc == 2 and "256" in msg
+
+
+def test_prefill_workspace_size():
+    lib = L.lib()
+    ws = lib.llkv_paged_prefill_workspace_size
+    # short key ranges: no chunking, no workspace
+    assert ws(8, 4096, 512, 1000, 14, 64, 16, 1) == 0
+    # configuration 4 (keys up to 4608): chunked, fp32 partials of 128 rows x (D + 1)
+    n = ws(8, 4096, 512, 4608, 14, 64, 16, 1)
+    assert n > 0 and n % (128 * 65 * 4) == 0
+    # fp32 pools use the generic kernel: no workspace
+    assert ws(8, 4096, 512, 4608, 14, 64, 16, 0) == 0
 
 
 def test_hash_tokens_abi():

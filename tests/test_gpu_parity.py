@@ -354,6 +354,20 @@ def test_prefill_config4_fp16():
     check_lowp(out, ref, "cfg4 prefill", 2e-3)
 
 
+def test_prefill_config4_unsplit_workspace():
+    """Without a workspace every key range runs unsplit; the result stays within the bar."""
+    say("prefill config 4 without workspace (no key chunks)")
+    case = wl.config4()
+    kp, vp = case.k_pool.to(DEV), case.v_pool.to(DEV)
+    kc.append_kv(case.k_chunk.to(DEV), case.v_chunk.to(DEV), case.slots.to(DEV), kp, vp)
+    out = kc.paged_prefill(case.q.to(DEV), kp, vp, case.block_table.to(DEV), case.cu_q.to(DEV),
+                           case.seq_lens.to(DEV), case.max_q_len, case.max_seq_len, causal=True,
+                           scale=case.scale, workspace=torch.empty(0, dtype=torch.uint8, device=DEV))
+    torch.cuda.synchronize()
+    ref = oracle_prefill(case, kp, vp)
+    check_lowp(out, ref, "cfg4 prefill unsplit", 2e-3)
+
+
 PREFILL = [
     # (name, Hq, Hkv, D, prefixes, chunks, dtype, causal)
     ("fp32_small_causal", 14, 2, 64, [0, 20, 33], [7, 64, 130], torch.float32, True),
@@ -366,6 +380,10 @@ PREFILL = [
     ("bf16_D64", 14, 2, 64, [16, 200], [100, 256], torch.bfloat16, True),
     ("bf16_D128", 32, 8, 128, [64], [200], torch.bfloat16, True),
     ("fp16_mha", 4, 4, 64, [31], [97], torch.float16, True),
+    # key ranges over 16 tiles (1024 keys): run as parallel chunks + merge
+    ("fp16_D64_long_noncausal", 14, 2, 64, [3000], [100], torch.float16, False),
+    ("bf16_D64_long", 14, 2, 64, [2500, 0], [300, 40], torch.bfloat16, True),
+    ("fp16_D128_long", 32, 8, 128, [2100], [130], torch.float16, True),
 ]
 
 
