@@ -20,7 +20,7 @@
 // keys sits at L - P + i and sees keys <= that position.
 //
 // Long key ranges are cut into chunks of kChunkTiles tiles, one work-group
-// each (grid: (N x qblocks x max_chunks, Hq)), so that a cached prefix of
+// each (grid: (Hq, N x qblocks x max_chunks)), so that a cached prefix of
 // thousands of keys does not serialise on one work-group; their fp32 partials
 // (normalised rows + log2-sum-exp2) are merged by prefill_merge_kernel.
 #pragma once
@@ -40,7 +40,7 @@ struct MfmaPrefillArgs {
     int max_blocks, N, Hq, Hkv, causal;
     float scale_log2;
     int qblocks;      // query blocks per sequence
-    int max_chunks;   // key chunks per (sequence, query block); grid.x = N * qblocks * max_chunks
+    int max_chunks;   // key chunks per (sequence, query block); grid.y = N * qblocks * max_chunks
     int chunk_tiles;  // key tiles per chunk
     float* part_o;    // [N*qblocks*max_chunks*Hq][BQ][D] (max_chunks > 1)
     float* part_lse;  // [N*qblocks*max_chunks*Hq][BQ]

@@ -25,6 +25,7 @@ template <> struct Mfma<_Float16> {
                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
     }
     __device__ static inline uint32_t pack2(float x, float y) { return pack_h2(x, y); }
+    static constexpr uint32_t kOnes = 0x3C003C00u;   // two halves of 1.0
 };
 
 template <> struct Mfma<bf16_t> {
@@ -34,19 +35,66 @@ template <> struct Mfma<bf16_t> {
                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
     }
     __device__ static inline uint32_t pack2(float x, float y) { return pack_b2(x, y); }
+    static constexpr uint32_t kOnes = 0x3F803F80u;   // two bfloat16 1.0
 };
 
 constexpr int BQ = 128;   // query rows per work-group
 constexpr int WQ = 32;    // query rows per wave (two 16-column MFMA tiles)
 constexpr int BN = 64;    // keys per tile (four pages)
 
+// Key tiles of unit u = (sequence n, query block): the causal extent of its
+// BQ rows over the sequence's keys.
+__device__ inline int unit_tiles(const MfmaPrefillArgs& a, int u) {
+    const int n = u / a.qblocks;
+    const int qb = a.qblocks - 1 - (u % a.qblocks);
+    const int q0 = a.cu_q[n];
+    const int P = a.cu_q[n + 1] - q0;
+    const int q_lo = qb * BQ;
+    if (q_lo >= P) return 0;
+    int L = a.lens[n];
+    const int cap = a.max_blocks * kPage;
+    L = L < 0 ? 0 : (L > cap ? cap : L);
+    int kend = a.causal ? L - P + min(q_lo + BQ, P) : L;
+    kend = kend < 0 ? 0 : (kend > L ? L : kend);
+    return (kend + BN - 1) / BN;
+}
+
+// Units ranked by key tiles (descending, ties by index) for up to kRankUnits
+// units; larger batches keep index order.  Every thread of the work-group
+// calls it (it contains barriers).
+constexpr int kRankUnits = 1024;
+
+__device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* order) {
+    const int U = a.N * a.qblocks;
+    if (U > kRankUnits) return rank;
+    int* tiles = order;
+    int* at = order + kRankUnits;
+    for (int u = threadIdx.x; u < U; u += blockDim.x) tiles[u] = unit_tiles(a, u);
+    __syncthreads();
+    for (int u = threadIdx.x; u < U; u += blockDim.x) {
+        const int tu = tiles[u];
+        int r = 0;
+        for (int v = 0; v < U; ++v) r += (tiles[v] > tu) | ((tiles[v] == tu) & (v < u));
+        at[r] = u;
+    }
+    __syncthreads();
+    return at[rank];
+}
+
+constexpr int kPageWindow = 256;   // page ids staged in LDS at a time
+
 template <int D>
 struct Smem {
     static constexpr int KPAD = D + 8;    // halves per K row (pad: spread LDS banks)
     static constexpr int VPAD = BN + 8;   // halves per V^T row
-    alignas(16) uint16_t k[2][BN * KPAD];
-    alignas(16) uint16_t vt[2][D * VPAD];
-    int pages[1024];   // page ids [tbase, tbase + 1024) of the sequence
+    union {
+        struct {
+            alignas(16) uint16_t k[2][BN * KPAD];
+            alignas(16) uint16_t vt[2][D * VPAD];
+        };
+        int order[2 * kRankUnits];   // prologue only: unit tiles, then unit at each rank
+    };
+    int pages[kPageWindow];   // page ids [tbase, tbase + kPageWindow) of the sequence
 };
 
 template <typename T, int D>
@@ -62,12 +110,18 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    const int hq = blockIdx.y;
+    // grid (Hq, ranked chunk slots): the dispatcher walks blockIdx.x fastest, so
+    // every head's work for a slot starts before the next slot's.  Work-groups
+    // run heaviest unit first: blockIdx.y / max_chunks is a rank in the
+    // descending order of the units' key tiles (longest-processing-time first,
+    // so long cached prefixes do not start last).
+    const int hq = blockIdx.x;
     const int kvh = hq / (a.Hq / a.Hkv);
-    const int unit = blockIdx.x / a.max_chunks;        // (sequence, query block)
-    const int ci = blockIdx.x - unit * a.max_chunks;   // key chunk of the unit
+    const int slot = blockIdx.y / a.max_chunks;
+    const int ci = blockIdx.y - slot * a.max_chunks;   // key chunk of the unit
+    const int unit = unit_by_rank(a, slot, sm.order);  // (sequence, query block)
     const int n = unit / a.qblocks;
-    const int qb = a.qblocks - 1 - (unit % a.qblocks);   // heavy (late) blocks first
+    const int qb = a.qblocks - 1 - (unit % a.qblocks);
 
     const int q0 = a.cu_q[n];
     const int P = a.cu_q[n + 1] - q0;
@@ -125,7 +179,10 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) o[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m[2] = {kNegBig, kNegBig};
-    float lsum[2] = {0.f, 0.f};
+    // Row sums of P on the MFMA: O^T's extra tile with an all-ones A operand;
+    // every element of osum[nt] is the running sum of query column c16.
+    f32x4 osum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const uint4 ones = make_uint4(Mfma<T>::kOnes, Mfma<T>::kOnes, Mfma<T>::kOnes, Mfma<T>::kOnes);
 
     // ---- staging: global -> registers -> LDS -----------------------------
     int tbase = 0;   // first page id held in sm.pages
@@ -137,7 +194,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         for (int j = 0; j < KCH_T; ++j) {
             const int ch = tid + 256 * j;
             const int key = ch / (D / 8), c = ch % (D / 8);
-            const int page = min((key0 + key) >> 4, last_page);
+            // pages past the sequence's last are staged as the last page (valid memory)
+            const int page = (key0 + key) >> 4;
             const int64_t row = (int64_t)max(sm.pages[page - tbase], 0) * kPage + ((key0 + key) & 15);
             kreg[j] = *reinterpret_cast<const u32x4*>(kg + row * row_elems + c * 8);
         }
@@ -146,7 +204,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             const int task = tid + 256 * j;
             const int kp = task % (BN / 2), c = task / (BN / 2);
             const int key = key0 + 2 * kp;
-            const int page = min(key >> 4, last_page);
+            const int page = key >> 4;
             const int64_t row = (int64_t)max(sm.pages[page - tbase], 0) * kPage + (key & 15);
             vreg[j][0] = *reinterpret_cast<const u32x4*>(vg + row * row_elems + c * 8);
             vreg[j][1] = *reinterpret_cast<const u32x4*>(vg + (row + 1) * row_elems + c * 8);
@@ -179,7 +237,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     // Page ids live in LDS so that no K/V load waits behind a table load.
     auto stage_pages = [&](int base) {
         tbase = base;
-        for (int i = tid; i < 1024; i += 256) sm.pages[i] = bt[min(base + i, last_page)];
+        for (int i = tid; i < kPageWindow; i += 256) sm.pages[i] = bt[min(base + i, last_page)];
         __syncthreads();
     };
     if (t_begin < t_end) {
@@ -194,7 +252,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         if (t + 1 < t_end) {
             // tile t+1 covers pages [4(t+1), 4(t+1)+4); restage when they leave the window
             // (uniform branch; every earlier read of sm.pages preceded the last barrier)
-            if (4 * (t + 1) + 4 > tbase + 1024) stage_pages(4 * (t + 1));
+            if (4 * (t + 1) + 4 > tbase + kPageWindow) stage_pages(4 * (t + 1));
             load_tile(t + 1, kr, vr);
         }
         __builtin_amdgcn_sched_barrier(0);   // next tile's loads issue before this tile's MFMAs
@@ -257,7 +315,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 const float mnew = fmaxf(m[nt], mx[nt]);
                 const float corr = fast_exp2(m[nt] - mnew);
                 m[nt] = mnew;
-                lsum[nt] *= corr;
+                osum[nt] *= corr;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= corr;
             }
@@ -265,16 +323,11 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         uint4 pop[2][2];   // P^T operands [k-step][query tile]
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            float ps = 0.f;
             float pv[4][4];
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    pv[kt][i] = fast_exp2(fmaf(s[kt][nt][i], c, -m[nt]));
-                    ps += pv[kt][i];
-                }
-            lsum[nt] += ps;
+                for (int i = 0; i < 4; ++i) pv[kt][i] = fast_exp2(fmaf(s[kt][nt][i], c, -m[nt]));
 #pragma unroll
             for (int ss = 0; ss < 2; ++ss) {
                 pop[ss][nt].x = Mfma<T>::pack2(pv[2 * ss][0], pv[2 * ss][1]);
@@ -295,6 +348,10 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 for (int nt = 0; nt < 2; ++nt) o[dt][nt] = Mfma<T>::mma(va, pop[ss][nt], o[dt][nt]);
             }
         }
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) osum[nt] = Mfma<T>::mma(ones, pop[ss][nt], osum[nt]);
 
         if (t + 1 < t_end) store_tile(buf ^ 1, kr, vr);
         __syncthreads();
@@ -307,9 +364,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const int64_t pidx = ((int64_t)unit * a.max_chunks + ci) * a.Hq + hq;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        float lt = lsum[nt];
-        lt += __shfl_xor(lt, 16, 64);
-        lt += __shfl_xor(lt, 32, 64);
+        const float lt = osum[nt][0];
         const int row = w * WQ + nt * 16 + c16;
         const int ql = q_lo + row;
         if (ql >= P) continue;
@@ -336,26 +391,21 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 }
 
 // Merge of a (sequence, query block, q head) unit's key chunks: grid
-// (N x qblocks, Hq, BQ / kMergeRows), 4 waves per work-group, kMergeRows / 4
-// rows per wave, lane d holding dims d, d + 64, ...  The loads of all the
-// wave's rows for kMergeBatch chunks are issued together; the log-sum-exp
-// weights are updated online per batch.
-constexpr int kMergeRows = 16;
-constexpr int kMergeBatch = 8;
-
+// (Hq, N x qblocks), 256 threads; thread (row, part) merges dims
+// [part * D/TPR, (part + 1) * D/TPR) of one row over the chunks with an online
+// log-sum-exp (each chunk's lse and row slice are loaded together).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
-    constexpr int MD = D / 64;
-    constexpr int RPW = kMergeRows / 4;   // rows per wave
-    const int unit = blockIdx.x, hq = blockIdx.y;
+    constexpr int TPR = 256 / BQ;     // threads per row
+    constexpr int V4 = D / TPR / 4;   // float4 per thread
+    const int hq = blockIdx.x, unit = blockIdx.y;
     const int n = unit / a.qblocks;
     const int qb = a.qblocks - 1 - (unit % a.qblocks);
     const int q0 = a.cu_q[n];
     const int P = a.cu_q[n + 1] - q0;
     const int q_lo = qb * BQ;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int row0 = blockIdx.z * kMergeRows + w * RPW;
-    if (q_lo + row0 >= P) return;
+    const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
+    if (q_lo + row >= P) return;
     int L = a.lens[n];
     const int cap = a.max_blocks * kPage;
     L = L < 0 ? 0 : (L > cap ? cap : L);
@@ -365,56 +415,38 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
     const int nchunks = (ntiles + a.chunk_tiles - 1) / a.chunk_tiles;
     if (nchunks <= 1) return;   // written directly
     const int64_t p0 = ((int64_t)unit * a.max_chunks) * a.Hq + hq;   // chunk c at p0 + c * Hq
-    const int nrows = min(RPW, P - q_lo - row0);
-    float M[RPW], W[RPW], acc[RPW][MD];
+    float M = -INFINITY, W = 0.0f;
+    float4 acc[V4];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        M[r] = -INFINITY;
-        W[r] = 0.0f;
+    for (int v = 0; v < V4; ++v) acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c = 0; c < nchunks; ++c) {
+        const int64_t pc = (p0 + (int64_t)c * a.Hq) * BQ + row;
+        const float l = a.part_lse[pc];
+        const float4* src = reinterpret_cast<const float4*>(a.part_o + pc * D) + part * V4;
+        float4 o[V4];
 #pragma unroll
-        for (int i = 0; i < MD; ++i) acc[r][i] = 0.0f;
-    }
-    for (int c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
-        float lv[RPW][kMergeBatch], pv[RPW][kMergeBatch][MD];
+        for (int v = 0; v < V4; ++v) o[v] = src[v];
+        const float Mn = fmaxf(M, l);
+        if (Mn == -INFINITY) continue;   // no key seen by this row yet
+        const float sc = fast_exp2(M - Mn), wt = fast_exp2(l - Mn);
+        W = fmaf(W, sc, wt);
 #pragma unroll
-        for (int r = 0; r < RPW; ++r)
-#pragma unroll
-            for (int j = 0; j < kMergeBatch; ++j) {
-                const bool ok = r < nrows && c0 + j < nchunks;
-                const int64_t pc = (p0 + (int64_t)(c0 + j) * a.Hq) * BQ + row0 + r;
-                lv[r][j] = ok ? a.part_lse[pc] : -INFINITY;
-#pragma unroll
-                for (int i = 0; i < MD; ++i) pv[r][j][i] = ok ? a.part_o[pc * D + lane + 64 * i] : 0.0f;
-            }
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            float mb = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < kMergeBatch; ++j) mb = fmaxf(mb, lv[r][j]);
-            const float Mn = fmaxf(M[r], mb);
-            if (Mn == -INFINITY) continue;   // no key seen by this row yet
-            const float sc = fast_exp2(M[r] - Mn);
-            W[r] *= sc;
-#pragma unroll
-            for (int i = 0; i < MD; ++i) acc[r][i] *= sc;
-#pragma unroll
-            for (int j = 0; j < kMergeBatch; ++j) {
-                const float wt = fast_exp2(lv[r][j] - Mn);
-                W[r] += wt;
-#pragma unroll
-                for (int i = 0; i < MD; ++i) acc[r][i] = fmaf(wt, pv[r][j][i], acc[r][i]);
-            }
-            M[r] = Mn;
+        for (int v = 0; v < V4; ++v) {
+            acc[v].x = fmaf(acc[v].x, sc, wt * o[v].x);
+            acc[v].y = fmaf(acc[v].y, sc, wt * o[v].y);
+            acc[v].z = fmaf(acc[v].z, sc, wt * o[v].z);
+            acc[v].w = fmaf(acc[v].w, sc, wt * o[v].w);
         }
+        M = Mn;
     }
-    T* og = reinterpret_cast<T*>(a.out);
+    const float inv = W > 0.f ? 1.0f / W : 0.f;
+    T* orow = reinterpret_cast<T*>(a.out) + ((int64_t)(q0 + q_lo + row) * a.Hq + hq) * D + part * V4 * 4;
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        if (r >= nrows) break;
-        const float inv = W[r] > 0.f ? 1.0f / W[r] : 0.f;
-        T* orow = og + ((int64_t)(q0 + q_lo + row0 + r) * a.Hq + hq) * D;
-#pragma unroll
-        for (int i = 0; i < MD; ++i) orow[lane + 64 * i] = Elem<T>::from_f32(acc[r][i] * inv);
+    for (int v = 0; v < V4; ++v) {
+        uint2 w2;
+        w2.x = Mfma<T>::pack2(acc[v].x * inv, acc[v].y * inv);
+        w2.y = Mfma<T>::pack2(acc[v].z * inv, acc[v].w * inv);
+        *reinterpret_cast<uint2*>(orow + 4 * v) = w2;
     }
 }
 
@@ -423,10 +455,13 @@ bool prefill_mfma_handles(int head_dim, int block_size, int dtype) {
            (head_dim == 64 || head_dim == 128);
 }
 
-// Key tiles per chunk: 16 tiles (1024 keys) keeps a work-group's run short
+// Key tiles per chunk: 24 tiles (1536 keys) keeps a work-group's run short
 // against the 256 CUs while a chunk's K/V traffic stays large against its
 // partial rows.
-constexpr int kChunkTiles = 16;
+#ifndef LLKV_PREFILL_CHUNK_TILES
+#define LLKV_PREFILL_CHUNK_TILES 24
+#endif
+constexpr int kChunkTiles = LLKV_PREFILL_CHUNK_TILES;
 
 struct ChunkPlan {
     int qblocks, max_chunks;
@@ -473,8 +508,8 @@ int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dty
         a.part_lse = nullptr;
         a.part_o = nullptr;
     }
-    dim3 grid(a.N * a.qblocks * a.max_chunks, a.Hq);
-    dim3 mgrid(a.N * a.qblocks, a.Hq, BQ / kMergeRows);
+    dim3 grid(a.Hq, a.N * a.qblocks * a.max_chunks);
+    dim3 mgrid(a.Hq, a.N * a.qblocks);
     const bool merge = a.max_chunks > 1;
     if (dtype == LLKV_DTYPE_F16) {
         if (head_dim == 64) {
