@@ -177,6 +177,9 @@ constexpr int kPage = 16;   // tokens per KV page (BLOCK of the reference)
 namespace llkv {
 int set_error(int status, const char* fmt, ...);
 int check_launch(const char* what);
+// Work-groups of `threads` threads of kernel `fn` the current device holds at
+// once (compute units x resident work-groups per unit), cached per device.
+int resident_workgroups(const void* fn, int threads);
 inline size_t dtype_bytes(int dtype) {
     return dtype == LLKV_DTYPE_F32 ? 4 : (dtype == LLKV_DTYPE_F16 || dtype == LLKV_DTYPE_BF16) ? 2 : 0;
 }

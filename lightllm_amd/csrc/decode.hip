@@ -430,26 +430,8 @@ BalancedWs balanced_workspace(int B, int Hq, int Hkv, int D) {
 
 bool balanced_eligible(int B) { return B <= kBalanceMaxB; }
 
-// Work-groups of kernel `fn` (256 threads) the current device holds at once:
-// compute units x resident work-groups per unit, cached per (device, kernel).
 int resident_wgs(DecodeFn fn) {
-    static std::mutex mu;
-    static std::map<std::pair<int, DecodeFn>, int> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find({dev, fn});
-    if (it != cache.end()) return it->second;
-    int cus = 0, per_cu = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
-                                                     64 * kDecodeWaves, 0) != hipSuccess ||
-        per_cu <= 0)
-        per_cu = 1;
-    const int cap = std::max(1, cus * per_cu);
-    cache[{dev, fn}] = cap;
-    return cap;
+    return resident_workgroups(reinterpret_cast<const void*>(fn), 64 * kDecodeWaves);
 }
 
 // Work-groups of the balanced schedule: one resident set (more only adds a

@@ -1,8 +1,12 @@
-// Thread-local error reporting for the C ABI.
+// Thread-local error reporting for the C ABI; device occupancy queries.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "common.h"
 
@@ -16,6 +20,24 @@ int set_error(int status, const char* fmt, ...) {
     vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
     va_end(ap);
     return status;
+}
+
+int resident_workgroups(const void* fn, int threads) {
+    static std::mutex mu;
+    static std::map<std::pair<int, const void*>, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({dev, fn});
+    if (it != cache.end()) return it->second;
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0) != hipSuccess || per_cu <= 0)
+        per_cu = 1;
+    const int cap = std::max(1, cus * per_cu);
+    cache[{dev, fn}] = cap;
+    return cap;
 }
 
 int check_launch(const char* what) {
