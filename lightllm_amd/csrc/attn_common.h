@@ -66,6 +66,8 @@ __device__ inline void lds_barrier() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+constexpr int kDecodeWaves = 4;   // waves per decode work-group
+
 constexpr float kNegBig = -1e30f;   // finite "minus infinity" for running maxima
 
 // A segment: pages [pg_begin, pg_begin + npages) of (sequence b, kv head

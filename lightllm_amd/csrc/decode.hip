@@ -5,26 +5,23 @@
 // host dispatcher (:537-626).  Math is the same online softmax; the mapping
 // to the hardware is new:
 //
-//  * One wave64 per (split, kv_head, sequence).  All G = Hq/Hkv query heads of
-//    the KV head are computed by that wave, so every K/V byte is read from
-//    HBM once (the reference launches one block per query head and re-reads
-//    K/V G times).
-//  * A token's row (D elements) is spread over LPT = D/8 lanes, 8 dims per
-//    lane, loaded as 16-byte global_load_dwordx4; 64/LPT tokens per step,
-//    8 (fp16/bf16) or 4 (fp32) steps in flight per tile: 16 outstanding
-//    dwordx4 loads per lane, no LDS round trip.
-//  * The per-token dot product is finished with DPP row reductions
-//    (quad_perm, row_half_mirror, row_mirror); each token group keeps its own
-//    running (max, sum, acc) so no cross-group traffic happens until the end
-//    of the split, where the groups are merged by log-sum-exp with shuffles.
-//  * Two schedules.  Fixed split (num_splits = S > 0): the reference's S
-//    ranges of ceil(n/S) pages per sequence, one work-group per (split, kv
-//    head, sequence).  Balanced (num_splits = 0): as many work-groups as the
-//    GPU holds at once, each taking an equal share of the batch's pages
-//    whatever the length mix (attn_common.h), so no work-group waits for a
-//    slot and none runs long.  Partials are merged by log-sum-exp in a small
-//    second kernel; a (sequence, kv head) computed by one work-group writes
-//    its output directly.
+//  * A work-group of 4 waves runs a segment: a page range of one (sequence,
+//    kv head).  All G = Hq/Hkv query heads of the kv head are computed
+//    together, so every K/V byte is read from HBM once (the reference
+//    launches one block per query head and re-reads K/V G times).
+//  * Scores and the weighted V sum are two small matrix products per page on
+//    the MFMA units (decode_mfma.h), with K/V loaded straight into the
+//    operand registers (16-byte K loads, 8- or 16-byte V loads); the 4 waves
+//    take interleaved pages and merge their softmax states through LDS.
+//  * Schedules.  Fixed split (num_splits = S > 0): the reference's S ranges
+//    of ceil(n/S) pages per sequence, one work-group per (split, kv head,
+//    sequence).  Automatic (num_splits = 0): fixed splits sized from the
+//    resident work-group count when the batch has few (sequence, kv head)
+//    units, else the balanced schedule -- as many work-groups as the GPU
+//    holds at once, each taking an equal share of the batch's pages whatever
+//    the length mix (attn_common.h).  Partials are merged by log-sum-exp in a
+//    small second kernel; a unit computed by one work-group writes its
+//    output directly.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -35,7 +32,6 @@
 #include <utility>
 
 #include "attn_common.h"
-#include "decode_fast.h"
 #include "decode_mfma.h"
 
 namespace llkv {
@@ -334,33 +330,35 @@ Kernels kernels_of() {
 }
 
 template <typename T, int D>
-Kernels pick_fast_g(int G) {
+Kernels pick_mfma16_g(int G) {
     switch (G) {
-        case 1: return kernels_of<FastDecode<T, D, 1>>();
-        case 2: return kernels_of<FastDecode<T, D, 2>>();
-        case 4: return kernels_of<FastDecode<T, D, 4>>();
-        case 7: return kernels_of<FastDecode<T, D, 7>>();
-        case 8: return kernels_of<FastDecode<T, D, 8>>();
+        case 1: return kernels_of<MfmaDecode<T, D, 1>>();
+        case 2: return kernels_of<MfmaDecode<T, D, 2>>();
+        case 4: return kernels_of<MfmaDecode<T, D, 4>>();
+        case 7: return kernels_of<MfmaDecode<T, D, 7>>();
+        case 8: return kernels_of<MfmaDecode<T, D, 8>>();
+        case 16: return kernels_of<MfmaDecode<T, D, 16>>();
     }
     return Kernels();
 }
 
+// fp16 / bf16 pools: the MFMA body (decode_mfma.h).
 template <typename T>
-Kernels pick_fast(int D, int G) {
-    if (D == 64) return pick_fast_g<T, 64>(G);
-    if (D == 128) return pick_fast_g<T, 128>(G);
+Kernels pick_mfma16(int D, int G) {
+    if (D == 64) return pick_mfma16_g<T, 64>(G);
+    if (D == 128) return pick_mfma16_g<T, 128>(G);
     return Kernels();
 }
 
 template <int D>
 Kernels pick_mfma_f32_g(int G) {
     switch (G) {
-        case 1: return kernels_of<MfmaF32Decode<D, 1>>();
-        case 2: return kernels_of<MfmaF32Decode<D, 2>>();
-        case 4: return kernels_of<MfmaF32Decode<D, 4>>();
-        case 7: return kernels_of<MfmaF32Decode<D, 7>>();
-        case 8: return kernels_of<MfmaF32Decode<D, 8>>();
-        case 16: return kernels_of<MfmaF32Decode<D, 16>>();
+        case 1: return kernels_of<MfmaDecode<float, D, 1>>();
+        case 2: return kernels_of<MfmaDecode<float, D, 2>>();
+        case 4: return kernels_of<MfmaDecode<float, D, 4>>();
+        case 7: return kernels_of<MfmaDecode<float, D, 7>>();
+        case 8: return kernels_of<MfmaDecode<float, D, 8>>();
+        case 16: return kernels_of<MfmaDecode<float, D, 16>>();
     }
     return Kernels();
 }
@@ -541,8 +539,8 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
     Kernels ks;
     if (block_size == kPage && aligned) {
         if (dtype == LLKV_DTYPE_F32) ks = pick_f32(head_dim, G);
-        else if (dtype == LLKV_DTYPE_F16) ks = pick_fast<_Float16>(head_dim, G);
-        else if (dtype == LLKV_DTYPE_BF16) ks = pick_fast<bf16_t>(head_dim, G);
+        else if (dtype == LLKV_DTYPE_F16) ks = pick_mfma16<_Float16>(head_dim, G);
+        else if (dtype == LLKV_DTYPE_BF16) ks = pick_mfma16<bf16_t>(head_dim, G);
     }
     const int max_pages_hint = (max_seq_len + block_size - 1) / block_size;
     bool balanced = false;

@@ -1,19 +1,24 @@
-// MFMA paged decode body for fp32 K/V on gfx950 (16-token pages, head_dim
-// 64 / 128, up to 16 query heads per KV head).  Included by decode.hip, which
-// instantiates it under the fixed-split and the balanced schedules.
+// MFMA paged decode body for fp32 / fp16 / bf16 K/V on gfx950 (16-token
+// pages, head_dim 64 / 128, up to 16 query heads per KV head).  Included by
+// decode.hip, which instantiates it under the fixed-split and the balanced
+// schedules.
 //
 // Per KV head the decode step is two small matrix products:
 //     S^T [tokens x G] = K [tokens x D] . Q^T [D x G]
 //     O^T [D x G]      = V^T [D x tokens] . P^T [tokens x G]
-// both run on v_mfma_f32_16x16x4_f32 (full fp32 products and sums), with the
-// G query heads as the 16-wide N dimension.  Operand layouts are chosen so
-// that nothing goes through LDS:
-//   * K: lane (g = lane/16, c = lane%16) holds token c of the page and, for
-//     k-step ks, dim 16*(ks/4) + 4*g + ks%4 -- four 16-byte loads per page;
+// with the G query heads as the 16-wide N dimension.  The second product runs
+// on v_mfma_f32_16x16x4_f32 (full fp32 products and sums; 16-bit V is widened
+// exactly), the first on v_mfma_f32_16x16x4_f32 for fp32 pools and on
+// v_mfma_f32_16x16x32_{f16,bf16} (exact products, fp32 sums) for 16-bit pools.
+// Operand layouts are chosen so that nothing goes through LDS:
+//   * K (fp32): lane (g = lane/16, c = lane%16) holds token c of the page and,
+//     for k-step ks, dim 16*(ks/4) + 4*g + ks%4 -- four 16-byte loads per page;
+//     (16-bit): token c, dims 32*ks + 8*g .. + 7, one 16-byte load per k-step;
 //   * S^T lands in lane (g, c) as tokens 4g+i (i < 4) of query c, which is
 //     exactly the B operand P^T of the second product for k-step i;
 //   * V^T: lane (g, c) loads V[token 4g+i][dims 64h + 4c .. 64h + 4c+3] as one
-//     16-byte load (16 lanes of a group read a 256-byte row segment); element
+//     16-byte (fp32) or 8-byte (16-bit) load, 16 lanes of a group reading one
+//     contiguous row segment; element
 //     j of that vector is the A operand of output tile dt = 4h + j, so tile dt
 //     row r holds dim 64h + 4r + j (a permutation undone when the tiles are
 //     written to LDS).
@@ -33,15 +38,113 @@
 namespace llkv {
 
 typedef float mf32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int mu32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int mu32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 mf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 mbf16x8 __attribute__((ext_vector_type(8)));
 
-template <int D, int G>
-struct MfmaF32Decode {
+// Score operands S^T = K Q^T per element type.  load_q fills the Q^T operand
+// of query column c (zero beyond G), load_k the K operand of token row c of a
+// page, scores returns the lane's 4 scores scaled into the exp2 domain.
+template <typename T, int D> struct ScoreOps;
+
+template <int D> struct ScoreOps<float, D> {
+    static constexpr int NQ = D / 4;    // one fp32 per k-step
+    static constexpr int NK = D / 16;   // float4 per page row
+    typedef float QReg;
+    typedef float4 KReg;
+    __device__ static void load_q(const float* qrow, bool valid, int g, float scale, QReg (&q)[NQ]) {
+#pragma unroll
+        for (int cc = 0; cc < NK; ++cc) {
+            float4 v = valid ? *reinterpret_cast<const float4*>(qrow + 16 * cc + 4 * g)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+            q[4 * cc + 0] = v.x * scale;
+            q[4 * cc + 1] = v.y * scale;
+            q[4 * cc + 2] = v.z * scale;
+            q[4 * cc + 3] = v.w * scale;
+        }
+    }
+    // krow: K row of the lane's token, at this kv head's dims
+    __device__ static void load_k(const float* krow, int g, KReg (&k)[NK]) {
+#pragma unroll
+        for (int cc = 0; cc < NK; ++cc) k[cc] = *reinterpret_cast<const float4*>(krow + 16 * cc + 4 * g);
+    }
+    __device__ static mf32x4 scores(const KReg (&k)[NK], const QReg (&q)[NQ], float) {
+        mf32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < NK; ++cc) {
+            s = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].x, q[4 * cc + 0], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].y, q[4 * cc + 1], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].z, q[4 * cc + 2], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].w, q[4 * cc + 3], s, 0, 0, 0);
+        }
+        return s;   // Q was pre-scaled
+    }
+    // V[row][dims 4c .. 4c+3] widened to fp32
+    __device__ static float4 load_v4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+};
+
+template <typename T16, int D> struct ScoreOps16 {
+    static constexpr int NQ = D / 32;   // 8 halves per k-step of 32 dims
+    static constexpr int NK = D / 32;
+    typedef mu32x4 QReg;
+    typedef mu32x4 KReg;
+    __device__ static void load_q(const T16* qrow, bool valid, int g, float, QReg (&q)[NQ]) {
+#pragma unroll
+        for (int ks = 0; ks < NQ; ++ks)
+            q[ks] = valid ? *reinterpret_cast<const mu32x4*>(qrow + 32 * ks + 8 * g) : mu32x4{0u, 0u, 0u, 0u};
+    }
+    __device__ static void load_k(const T16* krow, int g, KReg (&k)[NK]) {
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) k[ks] = *reinterpret_cast<const mu32x4*>(krow + 32 * ks + 8 * g);
+    }
+    __device__ static mf32x4 mma(const mu32x4& a, const mu32x4& b, mf32x4 c);
+    __device__ static mf32x4 scores(const KReg (&k)[NK], const QReg (&q)[NQ], float scale) {
+        mf32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) s = mma(k[ks], q[ks], s);
+        return s * scale;
+    }
+    __device__ static float4 load_v4(const T16* p) {
+        const mu32x2 w = *reinterpret_cast<const mu32x2*>(p);
+        float f[4];
+        if constexpr (sizeof(T16) == 2 && Elem<T16>::kDtype == LLKV_DTYPE_F16) {
+            unpack_h2(w.x, f);
+            unpack_h2(w.y, f + 2);
+        } else {
+            unpack_b2(w.x, f);
+            unpack_b2(w.y, f + 2);
+        }
+        return make_float4(f[0], f[1], f[2], f[3]);
+    }
+};
+
+template <>
+__device__ inline mf32x4 ScoreOps16<_Float16, 64>::mma(const mu32x4& a, const mu32x4& b, mf32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf16x8, a), __builtin_bit_cast(mf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ inline mf32x4 ScoreOps16<_Float16, 128>::mma(const mu32x4& a, const mu32x4& b, mf32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf16x8, a), __builtin_bit_cast(mf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ inline mf32x4 ScoreOps16<bf16_t, 64>::mma(const mu32x4& a, const mu32x4& b, mf32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mbf16x8, a), __builtin_bit_cast(mbf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ inline mf32x4 ScoreOps16<bf16_t, 128>::mma(const mu32x4& a, const mu32x4& b, mf32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mbf16x8, a), __builtin_bit_cast(mbf16x8, b), c, 0, 0, 0);
+}
+template <int D> struct ScoreOps<_Float16, D> : ScoreOps16<_Float16, D> {};
+template <int D> struct ScoreOps<bf16_t, D> : ScoreOps16<bf16_t, D> {};
+
+template <typename TT, int D, int G>
+struct MfmaDecode {
     static_assert(G >= 1 && G <= 16, "up to 16 query heads per KV head");
     static_assert(D % 64 == 0, "head_dim multiple of 64");
-    using T = float;
-    static constexpr int W = 4;               // waves per work-group
-    static constexpr int KC = D / 16;         // 16-byte K chunks per lane per page
-    static constexpr int KS = D / 4;          // k-steps of S^T = K Q^T
+    using T = TT;
+    using Ops = ScoreOps<T, D>;
+    static constexpr int W = kDecodeWaves;    // waves per work-group
     static constexpr int DT = D / 16;         // 16-dim tiles of O^T
     static constexpr int VH = D / 64;         // 16-byte V vectors per lane per token
     static constexpr int MD = (D + 63) / 64;
@@ -91,7 +194,7 @@ struct MfmaF32Decode {
         // State of the current segment.
         int cur = -1, sb = 0, skvh = 0, spg = 0, scum = 0, stok = 0;
         int next_cum = 0;   // first page of the next segment (register copy)
-        float qop[KS];
+        typename Ops::QReg qop[Ops::NQ];
         mf32x4 o[DT];
         float m = kNegBig, lsum = 0.0f;
 
@@ -114,7 +217,7 @@ struct MfmaF32Decode {
             }
         };
 
-        float4 kr[KC];
+        typename Ops::KReg kr[Ops::NK];
         float4 vr[VH][4];
         for (int k = 0;; ++k) {
             const int j = w + W * k;
@@ -134,18 +237,9 @@ struct MfmaF32Decode {
                 spg = segs[s].pg_begin;
                 scum = segs[s].cum;
                 stok = segs[s].tok_end;
-                // Q^T operand: column c is query head kvh*G + c (zero beyond G), pre-scaled.
-                const float* qrow = reinterpret_cast<const float*>(a.q) +
-                                    ((int64_t)sb * a.Hq + skvh * G + c) * D;
-#pragma unroll
-                for (int cc = 0; cc < KC; ++cc) {
-                    float4 v = c < G ? *reinterpret_cast<const float4*>(qrow + 16 * cc + 4 * g)
-                                     : make_float4(0.f, 0.f, 0.f, 0.f);
-                    qop[4 * cc + 0] = v.x * a.scale_log2;
-                    qop[4 * cc + 1] = v.y * a.scale_log2;
-                    qop[4 * cc + 2] = v.z * a.scale_log2;
-                    qop[4 * cc + 3] = v.w * a.scale_log2;
-                }
+                // Q^T operand: column c is query head kvh*G + c (zero beyond G).
+                const T* qrow = reinterpret_cast<const T*>(a.q) + ((int64_t)sb * a.Hq + skvh * G + c) * D;
+                Ops::load_q(qrow, c < G, g, a.scale_log2, qop);
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) o[dt] = mf32x4{0.f, 0.f, 0.f, 0.f};
                 m = kNegBig;
@@ -154,27 +248,18 @@ struct MfmaF32Decode {
             const int pg = spg + (j - scum);
             const int64_t phys = max(__builtin_amdgcn_readlane(tbl, k - tbl_k0), 0);
 
-            // K rows: lane (g, c) holds token c, dims 16 cc + 4 g .. + 3.
-            const float* kp = reinterpret_cast<const float*>(a.k) + (int64_t)skvh * D +
-                              (phys * kPage + c) * row_elems + 4 * g;
-#pragma unroll
-            for (int cc = 0; cc < KC; ++cc) kr[cc] = *reinterpret_cast<const float4*>(kp + 16 * cc);
+            // K row of the lane's token c; V rows 4g + i, dims 64h + 4c .. + 3.
+            const T* kp = reinterpret_cast<const T*>(a.k) + (int64_t)skvh * D + (phys * kPage + c) * row_elems;
+            Ops::load_k(kp, g, kr);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float* vp = reinterpret_cast<const float*>(a.v) + (int64_t)skvh * D +
-                                  (phys * kPage + 4 * g + i) * row_elems + 4 * c;
+                const T* vp = reinterpret_cast<const T*>(a.v) + (int64_t)skvh * D +
+                              (phys * kPage + 4 * g + i) * row_elems + 4 * c;
 #pragma unroll
-                for (int h = 0; h < VH; ++h) vr[h][i] = *reinterpret_cast<const float4*>(vp + 64 * h);
+                for (int h = 0; h < VH; ++h) vr[h][i] = Ops::load_v4(vp + 64 * h);
             }
 
-            mf32x4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int cc = 0; cc < KC; ++cc) {
-                sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[cc].x, qop[4 * cc + 0], sacc, 0, 0, 0);
-                sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[cc].y, qop[4 * cc + 1], sacc, 0, 0, 0);
-                sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[cc].z, qop[4 * cc + 2], sacc, 0, 0, 0);
-                sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[cc].w, qop[4 * cc + 3], sacc, 0, 0, 0);
-            }
+            const mf32x4 sacc = Ops::scores(kr, qop, a.scale_log2);
             const int t0 = pg * kPage + 4 * g;
             float x[4];
             float mt = kNegBig;
@@ -234,7 +319,8 @@ struct MfmaF32Decode {
                     for (int ww = 0; ww < W; ++ww) ov = fmaf(f[ww], sm.acc[s][ww][h][dd], ov);
                     ov *= inv;
                     if (d.direct)
-                        reinterpret_cast<float*>(a.out)[((int64_t)d.b * a.Hq + d.kvh * G + h) * D + dd] = ov;
+                        reinterpret_cast<T*>(a.out)[((int64_t)d.b * a.Hq + d.kvh * G + h) * D + dd] =
+                            Elem<T>::from_f32(ov);
                     else
                         a.part_o[d.po_off + h * po_stride + dd] = ov;
                 }
