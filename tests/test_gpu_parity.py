@@ -451,3 +451,42 @@ def test_cxx_api_gpu():
     r = subprocess.run([exe, "gpu"], capture_output=True, text=True, timeout=120)
     say(r.stdout + r.stderr)
     assert r.returncode == 0
+
+
+def _compact_pages(kp: torch.Tensor, vp: torch.Tensor, table: torch.Tensor):
+    """Host float32 copies of only the pages a table references, and the table renumbered
+    onto them (the full configuration 5 pool is 17 GB)."""
+    t = table.clone()
+    used = torch.unique(t[t >= 0])
+    remap = torch.full((kp.shape[0],), -1, dtype=torch.int32)
+    remap[used.long()] = torch.arange(used.numel(), dtype=torch.int32)
+    t[t >= 0] = remap[t[t >= 0].long()]
+    idx = used.long().to(kp.device)
+    return np_pool(kp.index_select(0, idx)), np_pool(vp.index_select(0, idx)), t
+
+
+def test_config5_mixed_step():
+    """Configuration 5 at full size, one step: append (256 decode tokens + 4 x 1024 chunk
+    tokens), decode of 256 lognormal contexts, then causal prefill of the chunks over a shared
+    2048-token prefix; Llama-3-8B heads (32/8/128), fp16, 262144-block pool."""
+    say("config 5 mixed step: append -> decode (256 seqs) -> prefill (4 x 1024 on 2048 shared)")
+    m = wl.config5()
+    dec, pre = m.decode, m.prefill
+    kp, vp = wl.device_pools(262144, 8, 128, torch.float16, 55, DEV)
+    kc.append_kv(dec.k_new.to(DEV), dec.v_new.to(DEV), dec.slots.to(DEV), kp, vp)
+    kc.append_kv(pre.k_chunk.to(DEV), pre.v_chunk.to(DEV), pre.slots.to(DEV), kp, vp)
+    out_d = kc.paged_decode(dec.q.to(DEV), kp, vp, dec.block_table.to(DEV), dec.seq_lens.to(DEV),
+                            dec.max_seq_len, scale=dec.scale)
+    out_p = kc.paged_prefill(pre.q.to(DEV), kp, vp, pre.block_table.to(DEV), pre.cu_q.to(DEV),
+                             pre.seq_lens.to(DEV), pre.max_q_len, pre.max_seq_len, causal=True,
+                             scale=pre.scale)
+    torch.cuda.synchronize()
+    kd, vd, td = _compact_pages(kp, vp, dec.block_table)
+    ref_d = oracle.paged_decode(dec.q.float().numpy(), kd, vd, td.numpy(), dec.seq_lens.numpy(),
+                                f64=True, nthreads=16)
+    check_lowp(out_d, ref_d, "cfg5 decode", 2e-3)
+    del kd, vd
+    kpp, vpp, tp = _compact_pages(kp, vp, pre.block_table)
+    ref_p = oracle.paged_prefill(pre.q.float().numpy(), pre.cu_q.numpy(), kpp, vpp, tp.numpy(),
+                                 pre.seq_lens.numpy(), True, f64=True, nthreads=16)
+    check_lowp(out_p, ref_p, "cfg5 prefill", 2e-3)
