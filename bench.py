@@ -194,6 +194,66 @@ def bench_prefill(args, torch, kc, wl):
     return {"us": us, "flop": flops, "tflops": tflops, "mfma_frac": tflops / FP16_MFMA_PEAK_TFLOPS}
 
 
+def _graph_us(torch, fn, n):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(n):
+                fn(i)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / n
+
+
+def bench_other_configs(torch, kc, wl):
+    """Configurations 3 and 5 (decode HBM rate, prefill MFMA rate), HIP-graph replays."""
+    dev = torch.device("cuda:0")
+    res = {}
+    c3 = wl.config3()
+    pools = [wl.device_pools(c3.k_pool.shape[0], 2, 64, torch.float16, 30 + i, dev) for i in range(2)]
+    q, bt, sl = c3.q.to(dev), c3.block_table.to(dev), c3.seq_lens.to(dev)
+    out = torch.empty_like(q)
+    for S in (0, 16):
+        us = _graph_us(torch, lambda i: kc.paged_decode(q, pools[i % 2][0], pools[i % 2][1], bt, sl,
+                                                       c3.max_seq_len, num_splits=S, out=out), 20)
+        res[f"cfg3_decode_S{S}"] = {"us": round(us, 2),
+                                    "GBps": round(wl.decode_bytes(c3) / (us * 1e-6) / 1e9, 1)}
+    del pools
+    m5 = wl.config5()
+    dec, pre = m5.decode, m5.prefill
+    kp, vp = wl.device_pools(262144, 8, 128, torch.float16, 55, dev)
+    dq, dbt, dsl = dec.q.to(dev), dec.block_table.to(dev), dec.seq_lens.to(dev)
+    kn, vn, dsl_slots = dec.k_new.to(dev), dec.v_new.to(dev), dec.slots.to(dev)
+    pq, pbt, pcu, psl = pre.q.to(dev), pre.block_table.to(dev), pre.cu_q.to(dev), pre.seq_lens.to(dev)
+    pk, pv, pslots = pre.k_chunk.to(dev), pre.v_chunk.to(dev), pre.slots.to(dev)
+    dout, pout = torch.empty_like(dq), torch.empty_like(pq)
+
+    def step(i):
+        kc.append_kv(kn, vn, dsl_slots, kp, vp)
+        kc.append_kv(pk, pv, pslots, kp, vp)
+        kc.paged_decode(dq, kp, vp, dbt, dsl, dec.max_seq_len, out=dout)
+        kc.paged_prefill(pq, kp, vp, pbt, pcu, psl, pre.max_q_len, pre.max_seq_len, True, out=pout)
+
+    step_us = _graph_us(torch, step, 5)
+    dec_us = _graph_us(torch, lambda i: kc.paged_decode(dq, kp, vp, dbt, dsl, dec.max_seq_len, out=dout), 5)
+    pre_us = _graph_us(torch, lambda i: kc.paged_prefill(pq, kp, vp, pbt, pcu, psl, pre.max_q_len,
+                                                         pre.max_seq_len, True, out=pout), 5)
+    pf = wl.prefill_flops(pre)
+    res["cfg5_step"] = {"us": round(step_us, 1), "decode_us": round(dec_us, 1),
+                        "decode_GBps": round(wl.decode_bytes(dec) / (dec_us * 1e-6) / 1e9, 1),
+                        "prefill_us": round(pre_us, 1),
+                        "prefill_mfma_frac": round(pf / (pre_us * 1e-6) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4)}
+    return res
+
+
 def cpu_baseline(dec, budget_s: float):
     """The oracle (reference CPU path restated in C: reconstruct_kv + cpu_attention) on
     configuration 2's layer-0 inputs, 1 thread, median of >= 5 runs after one warmup."""
@@ -349,6 +409,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--rocprof-summary", metavar="DIR")
     ap.add_argument("--rocprof-traffic", nargs=4, metavar="DIR")
@@ -373,6 +434,7 @@ def main():
 
     dec = bench_decode(args, torch, kc, wl)
     pre = None if args.no_prefill else bench_prefill(args, torch, kc, wl)
+    other = None if args.no_other_configs else bench_other_configs(torch, kc, wl)
     cpu = None if args.no_cpu_baseline else cpu_baseline(dec, args.cpu_budget)
 
     step_us = dec["step_ms"] * 1e3
@@ -414,6 +476,8 @@ def main():
     if pre is not None:
         line["prefill_cfg4"] = {"us": round(pre["us"], 2), "TFLOPs": round(pre["tflops"], 1),
                                 "mfma_frac": round(pre["mfma_frac"], 4), "flop": pre["flop"]}
+    if other is not None:
+        line["other_configs"] = other
     print(json.dumps(line), flush=True)
 
 
