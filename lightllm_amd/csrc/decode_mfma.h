@@ -162,7 +162,8 @@ struct MfmaDecode {
 
     __device__ static void round(const DecodeArgs& a, Smem& sm, const SegDesc* segs, int nseg,
                                  int64_t po_stride, int64_t pl_stride) {
-        const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+        const int tid = threadIdx.x, lane = tid & 63;
+        const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, known uniform
         const int g = lane >> 4, c = lane & 15;
         const int np_total = segs[nseg - 1].cum + segs[nseg - 1].npages;
         const int64_t row_elems = (int64_t)a.Hkv * D;

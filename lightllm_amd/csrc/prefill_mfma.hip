@@ -108,7 +108,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     __shared__ Smem<D> sm;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, known uniform
     const int g = lane >> 4, c16 = lane & 15;
     // grid (Hq, ranked chunk slots): the dispatcher walks blockIdx.x fastest, so
     // every head's work for a slot starts before the next slot's.  Work-groups
@@ -140,7 +141,6 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const bool direct = nchunks <= 1;
     const int last_page = L > 0 ? (L - 1) / kPage : 0;
     const int* bt = a.bt + (int64_t)n * a.max_blocks;
-    const int64_t row_elems = (int64_t)a.Hkv * D;
     const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)kvh * D;
     const T* vg = reinterpret_cast<const T*>(a.v) + (int64_t)kvh * D;
 
@@ -188,26 +188,42 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     int tbase = 0;   // first page id held in sm.pages
     u32x4 kr[KCH_T];
     u32x4 vr[VT_T][2];
+    // Per-thread byte offsets inside a page and page slot of each staged row;
+    // a load is then base + phys * page_bytes + offset (one 32x32->64 multiply-add).
+    const uint32_t row_bytes = (uint32_t)(a.Hkv * D * sizeof(T));
+    const uint32_t page_bytes = row_bytes * kPage;
+    const char* kb = reinterpret_cast<const char*>(kg);
+    const char* vb = reinterpret_cast<const char*>(vg);
+    uint32_t koff[KCH_T], voff[VT_T];
+    int kslot[KCH_T], vslot[VT_T];
+#pragma unroll
+    for (int j = 0; j < KCH_T; ++j) {
+        const int ch = tid + 256 * j;
+        const int key = ch / (D / 8), c = ch % (D / 8);
+        kslot[j] = key >> 4;
+        koff[j] = (uint32_t)(key & 15) * row_bytes + (uint32_t)c * 16u;
+    }
+#pragma unroll
+    for (int j = 0; j < VT_T; ++j) {
+        const int task = tid + 256 * j;
+        const int kp = task % (BN / 2), c = task / (BN / 2);
+        vslot[j] = (2 * kp) >> 4;
+        voff[j] = (uint32_t)((2 * kp) & 15) * row_bytes + (uint32_t)c * 16u;
+    }
     auto load_tile = [&](int t, u32x4 (&kreg)[KCH_T], u32x4 (&vreg)[VT_T][2]) {
-        const int key0 = t * BN;
+        // pages past the sequence's last are staged as the last page (valid memory)
+        const int* pg = sm.pages + (4 * t - tbase);
 #pragma unroll
         for (int j = 0; j < KCH_T; ++j) {
-            const int ch = tid + 256 * j;
-            const int key = ch / (D / 8), c = ch % (D / 8);
-            // pages past the sequence's last are staged as the last page (valid memory)
-            const int page = (key0 + key) >> 4;
-            const int64_t row = (int64_t)max(sm.pages[page - tbase], 0) * kPage + ((key0 + key) & 15);
-            kreg[j] = *reinterpret_cast<const u32x4*>(kg + row * row_elems + c * 8);
+            const uint64_t phys = (uint32_t)max(pg[kslot[j]], 0);
+            kreg[j] = *reinterpret_cast<const u32x4*>(kb + phys * page_bytes + koff[j]);
         }
 #pragma unroll
         for (int j = 0; j < VT_T; ++j) {
-            const int task = tid + 256 * j;
-            const int kp = task % (BN / 2), c = task / (BN / 2);
-            const int key = key0 + 2 * kp;
-            const int page = key >> 4;
-            const int64_t row = (int64_t)max(sm.pages[page - tbase], 0) * kPage + (key & 15);
-            vreg[j][0] = *reinterpret_cast<const u32x4*>(vg + row * row_elems + c * 8);
-            vreg[j][1] = *reinterpret_cast<const u32x4*>(vg + (row + 1) * row_elems + c * 8);
+            const uint64_t phys = (uint32_t)max(pg[vslot[j]], 0);
+            const char* p = vb + phys * page_bytes + voff[j];
+            vreg[j][0] = *reinterpret_cast<const u32x4*>(p);
+            vreg[j][1] = *reinterpret_cast<const u32x4*>(p + row_bytes);
         }
     };
     auto store_tile = [&](int buf, const u32x4 (&kreg)[KCH_T], const u32x4 (&vreg)[VT_T][2]) {
