@@ -42,34 +42,60 @@ constexpr int BQ = 128;   // query rows per work-group
 constexpr int WQ = 32;    // query rows per wave (two 16-column MFMA tiles)
 constexpr int BN = 64;    // keys per tile (four pages)
 
-// Key tiles of unit u = (sequence n, query block): the causal extent of its
-// BQ rows over the sequence's keys.
-__device__ inline int unit_tiles(const MfmaPrefillArgs& a, int u) {
+// Unit u = (sequence n, query block qb): its query rows [q_lo, q_lo + BQ) of
+// the sequence's P new tokens (starting at row q0 of q) over L keys, and its
+// key tiles (the causal extent of the rows).  Query blocks are numbered from
+// the last, so that in a sequence the longest unit comes first.
+struct UnitInfo {
+    int q0, P, L, tiles;
+};
+
+__device__ inline UnitInfo unit_info(const MfmaPrefillArgs& a, int u) {
     const int n = u / a.qblocks;
     const int qb = a.qblocks - 1 - (u % a.qblocks);
-    const int q0 = a.cu_q[n];
-    const int P = a.cu_q[n + 1] - q0;
-    const int q_lo = qb * BQ;
-    if (q_lo >= P) return 0;
+    UnitInfo r;
+    r.q0 = a.cu_q[n];
+    r.P = a.cu_q[n + 1] - r.q0;
     int L = a.lens[n];
     const int cap = a.max_blocks * kPage;
-    L = L < 0 ? 0 : (L > cap ? cap : L);
-    int kend = a.causal ? L - P + min(q_lo + BQ, P) : L;
-    kend = kend < 0 ? 0 : (kend > L ? L : kend);
-    return (kend + BN - 1) / BN;
+    r.L = L < 0 ? 0 : (L > cap ? cap : L);
+    const int q_lo = qb * BQ;
+    if (q_lo >= r.P) {
+        r.tiles = 0;
+        return r;
+    }
+    int kend = a.causal ? r.L - r.P + min(q_lo + BQ, r.P) : r.L;
+    kend = kend < 0 ? 0 : (kend > r.L ? r.L : kend);
+    r.tiles = (kend + BN - 1) / BN;
+    return r;
 }
 
 // Units ranked by key tiles (descending, ties by index) for up to kRankUnits
 // units; larger batches keep index order.  Every thread of the work-group
-// calls it (it contains barriers).
+// calls it (it contains barriers).  Returns the unit of the given rank and
+// its UnitInfo (read back from LDS, so that the unit's lengths cost no second
+// global round trip).
 constexpr int kRankUnits = 1024;
 
-__device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* order) {
+__device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* order,
+                                   UnitInfo& info) {
     const int U = a.N * a.qblocks;
-    if (U > kRankUnits) return rank;
+    if (U > kRankUnits) {
+        info = unit_info(a, rank);
+        return rank;
+    }
     int* tiles = order;
     int* at = order + kRankUnits;
-    for (int u = threadIdx.x; u < U; u += blockDim.x) tiles[u] = unit_tiles(a, u);
+    int* q0s = order + 2 * kRankUnits;
+    int* ps = order + 3 * kRankUnits;
+    int* ls = order + 4 * kRankUnits;
+    for (int u = threadIdx.x; u < U; u += blockDim.x) {
+        const UnitInfo r = unit_info(a, u);
+        tiles[u] = r.tiles;
+        q0s[u] = r.q0;
+        ps[u] = r.P;
+        ls[u] = r.L;
+    }
     __syncthreads();
     for (int u = threadIdx.x; u < U; u += blockDim.x) {
         const int tu = tiles[u];
@@ -78,8 +104,17 @@ __device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* orde
         at[r] = u;
     }
     __syncthreads();
-    return at[rank];
+    const int u = at[rank];
+    info.q0 = q0s[u];
+    info.P = ps[u];
+    info.L = ls[u];
+    info.tiles = tiles[u];
+    return u;
 }
+
+#ifndef LLKV_PREFILL_INTERLEAVE
+#define LLKV_PREFILL_INTERLEAVE 1
+#endif
 
 constexpr int kPageWindow = 256;   // page ids staged in LDS at a time
 
@@ -92,7 +127,7 @@ struct Smem {
             alignas(16) uint16_t k[2][BN * KPAD];
             alignas(16) uint16_t vt[2][D * VPAD];
         };
-        int order[2 * kRankUnits];   // prologue only: unit tiles, then unit at each rank
+        int order[5 * kRankUnits];   // prologue only: unit tiles, unit at each rank, q0, P, L
     };
     int pages[kPageWindow];   // page ids [tbase, tbase + kPageWindow) of the sequence
 };
@@ -120,17 +155,16 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const int kvh = hq / (a.Hq / a.Hkv);
     const int slot = blockIdx.y / a.max_chunks;
     const int ci = blockIdx.y - slot * a.max_chunks;   // key chunk of the unit
-    const int unit = unit_by_rank(a, slot, sm.order);  // (sequence, query block)
+    UnitInfo ui;
+    const int unit = unit_by_rank(a, slot, sm.order, ui);  // (sequence, query block)
     const int n = unit / a.qblocks;
     const int qb = a.qblocks - 1 - (unit % a.qblocks);
 
-    const int q0 = a.cu_q[n];
-    const int P = a.cu_q[n + 1] - q0;
+    const int q0 = ui.q0;
+    const int P = ui.P;
     const int q_lo = qb * BQ;
     if (q_lo >= P) return;
-    int L = a.lens[n];
-    const int cap = a.max_blocks * kPage;
-    L = L < 0 ? 0 : (L > cap ? cap : L);
+    const int L = ui.L;
     int kend = a.causal ? L - P + min(q_lo + BQ, P) : L;
     kend = kend < 0 ? 0 : (kend > L ? L : kend);
     const int ntiles = (kend + BN - 1) / BN;
@@ -315,20 +349,23 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v = fmaxf(v, s[kt][nt][i]);
-            v = fmaxf(v, __shfl_xor(v, 16, 64));
-            v = fmaxf(v, __shfl_xor(v, 32, 64));
-            mx[nt] = v * c;
+            mx[nt] = v * c;   // this lane's 16 keys only
         }
-        // Lazy rescaling: the running max m only moves when a row's tile max
-        // exceeds it by more than 8 (so p <= 2^8 otherwise); then the whole wave
-        // rescales its accumulators once.  Usually only the first tile does.
+        // Lazy rescaling: the running max m only moves when some lane's tile
+        // max exceeds it by more than 8 (so p <= 2^8 otherwise); then the wave
+        // reduces the row maxima over the 4 lanes of each query column and
+        // rescales its accumulators once.  Usually only the first tile does, so
+        // the common path has no cross-lane traffic.
         bool grow = false;
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) grow |= mx[nt] > m[nt] + 8.0f;
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
-                const float mnew = fmaxf(m[nt], mx[nt]);
+                float v = mx[nt];
+                v = fmaxf(v, __shfl_xor(v, 16, 64));
+                v = fmaxf(v, __shfl_xor(v, 32, 64));
+                const float mnew = fmaxf(m[nt], v);
                 const float corr = fast_exp2(m[nt] - mnew);
                 m[nt] = mnew;
                 osum[nt] *= corr;
@@ -336,38 +373,89 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= corr;
             }
         }
-        uint4 pop[2][2];   // P^T operands [k-step][query tile]
+        // ---- P = 2^(S c - m) and O^T += V^T P^T, one 32-key half after the
+        // other: the second half's exponentials are interleaved with the first
+        // half's MFMAs, so that the VALU and the matrix core work together.
+        uint4 pop[2][2];   // P^T operands [k-step = key half][query tile]
+        auto softmax_half = [&](int ss) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            float pv[4][4];
+            for (int nt = 0; nt < 2; ++nt) {
+                float pv[2][4];
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+                for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) pv[kt][i] = fast_exp2(fmaf(s[kt][nt][i], c, -m[nt]));
-#pragma unroll
-            for (int ss = 0; ss < 2; ++ss) {
-                pop[ss][nt].x = Mfma<T>::pack2(pv[2 * ss][0], pv[2 * ss][1]);
-                pop[ss][nt].y = Mfma<T>::pack2(pv[2 * ss][2], pv[2 * ss][3]);
-                pop[ss][nt].z = Mfma<T>::pack2(pv[2 * ss + 1][0], pv[2 * ss + 1][1]);
-                pop[ss][nt].w = Mfma<T>::pack2(pv[2 * ss + 1][2], pv[2 * ss + 1][3]);
+                    for (int i = 0; i < 4; ++i)
+                        pv[h][i] = fast_exp2(fmaf(s[2 * ss + h][nt][i], c, -m[nt]));
+                pop[ss][nt].x = Mfma<T>::pack2(pv[0][0], pv[0][1]);
+                pop[ss][nt].y = Mfma<T>::pack2(pv[0][2], pv[0][3]);
+                pop[ss][nt].z = Mfma<T>::pack2(pv[1][0], pv[1][1]);
+                pop[ss][nt].w = Mfma<T>::pack2(pv[1][2], pv[1][3]);
             }
-        }
-
-        // ---- O^T += V^T P^T ------------------------------------------------
+        };
+        auto pv_half = [&](int ss) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-            for (int ss = 0; ss < 2; ++ss) {
+            for (int dt = 0; dt < DT; ++dt) {
                 const uint4 va = *reinterpret_cast<const uint4*>(
                     &sm.vt[buf][(dt * 16 + c16) * VPAD + 32 * ss + 8 * g]);
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) o[dt][nt] = Mfma<T>::mma(va, pop[ss][nt], o[dt][nt]);
             }
-        }
-#pragma unroll
-        for (int ss = 0; ss < 2; ++ss)
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) osum[nt] = Mfma<T>::mma(ones, pop[ss][nt], osum[nt]);
+        };
+#if LLKV_PREFILL_INTERLEAVE
+        // The first half's MFMAs, each followed by a share of the second half's
+        // exponentials; sched_barrier keeps this order (the scheduler would
+        // otherwise put all VALU work first).  V^T rows of the second half are
+        // read as those of the first are consumed.
+        softmax_half(0);
+        {
+            constexpr int kMf = 2 * DT + 2;   // MFMAs per half
+            uint4 va0[DT], va1[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                va0[dt] = *reinterpret_cast<const uint4*>(&sm.vt[buf][(dt * 16 + c16) * VPAD + 8 * g]);
+            float pv1[2][2][4];   // [query tile][h][i] of the second half
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < kMf; ++k) {
+                if (k < 2 * DT) {
+                    const int dt = k >> 1, nt = k & 1;
+                    o[dt][nt] = Mfma<T>::mma(va0[dt], pop[0][nt], o[dt][nt]);
+                    if (nt == 1)
+                        va1[dt] = *reinterpret_cast<const uint4*>(
+                            &sm.vt[buf][(dt * 16 + c16) * VPAD + 32 + 8 * g]);
+                } else {
+                    const int nt = k - 2 * DT;
+                    osum[nt] = Mfma<T>::mma(ones, pop[0][nt], osum[nt]);
+                }
+#pragma unroll
+                for (int e = k * 16 / kMf; e < (k + 1) * 16 / kMf; ++e) {
+                    const int nt = e >> 3, h = (e >> 2) & 1, i = e & 3;
+                    pv1[nt][h][i] = fast_exp2(fmaf(s[2 + h][nt][i], c, -m[nt]));
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                pop[1][nt].x = Mfma<T>::pack2(pv1[nt][0][0], pv1[nt][0][1]);
+                pop[1][nt].y = Mfma<T>::pack2(pv1[nt][0][2], pv1[nt][0][3]);
+                pop[1][nt].z = Mfma<T>::pack2(pv1[nt][1][0], pv1[nt][1][1]);
+                pop[1][nt].w = Mfma<T>::pack2(pv1[nt][1][2], pv1[nt][1][3]);
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) o[dt][nt] = Mfma<T>::mma(va1[dt], pop[1][nt], o[dt][nt]);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) osum[nt] = Mfma<T>::mma(ones, pop[1][nt], osum[nt]);
+        }
+#else
+        softmax_half(0);
+        pv_half(0);
+        softmax_half(1);
+        pv_half(1);
+#endif
 
         if (t + 1 < t_end) store_tile(buf ^ 1, kr, vr);
         __syncthreads();
