@@ -19,10 +19,12 @@
 // Causal masking uses the reference's rule: query i of a P-row chunk over L
 // keys sits at L - P + i and sees keys <= that position.
 //
-// Long key ranges are cut into chunks of kChunkTiles tiles, one work-group
-// each (grid: (Hq, N x qblocks x max_chunks)), so that a cached prefix of
-// thousands of keys does not serialise on one work-group; their fp32 partials
-// (normalised rows + log2-sum-exp2) are merged by prefill_merge_kernel.
+// When the units alone would not fill the GPU, key ranges are cut into chunks
+// of chunk_tiles tiles, one work-group each (grid: (Hq, N x qblocks x
+// max_chunks)), so that a cached prefix of thousands of keys does not
+// serialise on one work-group; their fp32 partials (normalised rows +
+// log2-sum-exp2) are merged by prefill_merge_kernel.  The split is chosen on
+// the host from the shape bounds and the kernel's resident work-group count.
 #pragma once
 
 #include "attn_common.h"

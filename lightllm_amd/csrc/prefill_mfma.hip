@@ -559,24 +559,43 @@ bool prefill_mfma_handles(int head_dim, int block_size, int dtype) {
            (head_dim == 64 || head_dim == 128);
 }
 
-// Key tiles per chunk: 24 tiles (1536 keys) keeps a work-group's run short
-// against the 256 CUs while a chunk's K/V traffic stays large against its
-// partial rows.
-#ifndef LLKV_PREFILL_CHUNK_TILES
-#define LLKV_PREFILL_CHUNK_TILES 24
+// Key-range split.  When the (sequence, query block, q head) units alone
+// would leave the GPU idle, a unit's key tiles are cut into chunks of
+// ceil(max_tiles / k) tiles, k chosen so that the launch offers about kFill
+// work-groups per resident slot (counted as if every unit had the longest key
+// range), with chunks of at least kMinChunkTiles tiles.  With enough units
+// (k = 1) nothing is split: no partials and no merge.
+#ifndef LLKV_PREFILL_FILL
+#define LLKV_PREFILL_FILL 1.5
 #endif
-constexpr int kChunkTiles = LLKV_PREFILL_CHUNK_TILES;
+constexpr double kFill = LLKV_PREFILL_FILL;
+constexpr int kMinChunkTiles = 8;
+
+const void* prefill_kernel_fn(int dtype, int head_dim) {
+    if (dtype == LLKV_DTYPE_F16)
+        return head_dim == 64 ? reinterpret_cast<const void*>(prefill_mfma_kernel<_Float16, 64>)
+                              : reinterpret_cast<const void*>(prefill_mfma_kernel<_Float16, 128>);
+    return head_dim == 64 ? reinterpret_cast<const void*>(prefill_mfma_kernel<bf16_t, 64>)
+                          : reinterpret_cast<const void*>(prefill_mfma_kernel<bf16_t, 128>);
+}
 
 struct ChunkPlan {
-    int qblocks, max_chunks;
+    int qblocks, max_chunks, chunk_tiles;
 };
 
-ChunkPlan chunk_plan(int total_q, int max_q_len, int max_seq_len) {
+ChunkPlan chunk_plan(int N, int Hq, int head_dim, int dtype, int total_q, int max_q_len,
+                     int max_seq_len) {
     ChunkPlan c;
     const int qmax = (max_q_len > 0 && max_q_len < total_q) ? max_q_len : total_q;
     c.qblocks = (qmax + BQ - 1) / BQ;
     const int max_tiles = (std::max(max_seq_len, 1) + BN - 1) / BN;
-    c.max_chunks = std::max(1, (max_tiles + kChunkTiles - 1) / kChunkTiles);
+    const double unit_heads = (double)N * c.qblocks * Hq;
+    const int slots = resident_workgroups(prefill_kernel_fn(dtype, head_dim), 256);
+    int k = (int)std::ceil(kFill * slots / unit_heads);
+    k = std::min(k, std::max(1, max_tiles / kMinChunkTiles));
+    k = std::max(k, 1);
+    c.chunk_tiles = (max_tiles + k - 1) / k;
+    c.max_chunks = (max_tiles + c.chunk_tiles - 1) / c.chunk_tiles;
     return c;
 }
 
@@ -585,7 +604,7 @@ ChunkPlan chunk_plan(int total_q, int max_q_len, int max_seq_len) {
 size_t prefill_mfma_workspace(int N, int Hq, int head_dim, int block_size, int dtype, int total_q,
                               int max_q_len, int max_seq_len) {
     if (!prefill_mfma_handles(head_dim, block_size, dtype) || N <= 0 || total_q <= 0) return 0;
-    const ChunkPlan c = chunk_plan(total_q, max_q_len, max_seq_len);
+    const ChunkPlan c = chunk_plan(N, Hq, head_dim, dtype, total_q, max_q_len, max_seq_len);
     if (c.max_chunks <= 1) return 0;
     const size_t parts = (size_t)N * c.qblocks * c.max_chunks * Hq;
     return parts * BQ * sizeof(float) + parts * BQ * head_dim * sizeof(float);
@@ -596,14 +615,14 @@ int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dty
                         size_t workspace_bytes, hipStream_t st) {
     if (!prefill_mfma_handles(head_dim, block_size, dtype)) return -1;
     if (((uintptr_t)a.q | (uintptr_t)a.out | (uintptr_t)a.k | (uintptr_t)a.v) & 15) return -1;
-    const ChunkPlan c = chunk_plan(total_q, max_q_len, max_seq_len);
+    const ChunkPlan c = chunk_plan(a.N, a.Hq, head_dim, dtype, total_q, max_q_len, max_seq_len);
     a.qblocks = c.qblocks;
     const size_t need = prefill_mfma_workspace(a.N, a.Hq, head_dim, block_size, dtype, total_q,
                                                max_q_len, max_seq_len);
     if (need > 0 && workspace != nullptr && workspace_bytes >= need) {
         const size_t parts = (size_t)a.N * c.qblocks * c.max_chunks * a.Hq;
         a.max_chunks = c.max_chunks;
-        a.chunk_tiles = kChunkTiles;
+        a.chunk_tiles = c.chunk_tiles;
         a.part_lse = reinterpret_cast<float*>(workspace);
         a.part_o = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + parts * BQ * sizeof(float));
     } else {   // no (or too small a) workspace: one chunk per unit
