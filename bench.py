@@ -172,29 +172,15 @@ def bench_prefill(args, torch, kc, wl):
     for _ in range(5):
         run()
     torch.cuda.synchronize()
-    n = max(20, args.steps // 4)
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(side):
-        with torch.cuda.graph(graph, stream=side):
-            for _ in range(n):
-                run()
-    torch.cuda.synchronize()
-    graph.replay()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    graph.replay()
-    b.record()
-    torch.cuda.synchronize()
-    us = a.elapsed_time(b) * 1e3 / n
+    us = _graph_us(torch, lambda i: run(), max(20, args.steps // 4))
     flops = wl.prefill_flops(case)
     tflops = flops / (us * 1e-6) / 1e12
     return {"us": us, "flop": flops, "tflops": tflops, "mfma_frac": tflops / FP16_MFMA_PEAK_TFLOPS}
 
 
-def _graph_us(torch, fn, n):
+def _graph_us(torch, fn, n, warm_replays=3, timed_replays=5):
+    """Per-call time of fn over a HIP graph of n calls: warm replays, then the
+    median of timed replays (each bracketed by HIP events on the launch stream)."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
@@ -203,14 +189,18 @@ def _graph_us(torch, fn, n):
             for i in range(n):
                 fn(i)
     torch.cuda.synchronize()
-    graph.replay()
+    for _ in range(warm_replays):
+        graph.replay()
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    graph.replay()
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) * 1e3 / n
+    times = []
+    for _ in range(timed_replays):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) * 1e3 / n)
+    return statistics.median(times)
 
 
 def bench_other_configs(torch, kc, wl):
