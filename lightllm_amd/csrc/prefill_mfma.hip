@@ -564,12 +564,16 @@ bool prefill_mfma_handles(int head_dim, int block_size, int dtype) {
 // ceil(max_tiles / k) tiles, k chosen so that the launch offers about kFill
 // work-groups per resident slot (counted as if every unit had the longest key
 // range), with chunks of at least kMinChunkTiles tiles.  With enough units
-// (k = 1) nothing is split: no partials and no merge.
+// (k = 1) nothing is split: no partials and no merge.  The workspace is sized
+// from the shape alone, for kSizingSlots resident slots (256 CUs x 4
+// work-groups, above what this kernel reaches); a launch takes the smaller of
+// that k and the one of its device's actual resident count.
 #ifndef LLKV_PREFILL_FILL
 #define LLKV_PREFILL_FILL 1.5
 #endif
 constexpr double kFill = LLKV_PREFILL_FILL;
 constexpr int kMinChunkTiles = 8;
+constexpr int kSizingSlots = 1024;
 
 const void* prefill_kernel_fn(int dtype, int head_dim) {
     if (dtype == LLKV_DTYPE_F16)
@@ -583,17 +587,21 @@ struct ChunkPlan {
     int qblocks, max_chunks, chunk_tiles;
 };
 
-ChunkPlan chunk_plan(int N, int Hq, int head_dim, int dtype, int total_q, int max_q_len,
-                     int max_seq_len) {
+// slots <= 0: size for kSizingSlots; otherwise the launch plan for that many
+// resident slots (never more chunks than the sizing plan).
+ChunkPlan chunk_plan(int N, int Hq, int total_q, int max_q_len, int max_seq_len, int slots) {
     ChunkPlan c;
     const int qmax = (max_q_len > 0 && max_q_len < total_q) ? max_q_len : total_q;
     c.qblocks = (qmax + BQ - 1) / BQ;
     const int max_tiles = (std::max(max_seq_len, 1) + BN - 1) / BN;
     const double unit_heads = (double)N * c.qblocks * Hq;
-    const int slots = resident_workgroups(prefill_kernel_fn(dtype, head_dim), 256);
-    int k = (int)std::ceil(kFill * slots / unit_heads);
-    k = std::min(k, std::max(1, max_tiles / kMinChunkTiles));
-    k = std::max(k, 1);
+    auto splits = [&](int s) {
+        int k = (int)std::ceil(kFill * s / unit_heads);
+        k = std::min(k, std::max(1, max_tiles / kMinChunkTiles));
+        return std::max(k, 1);
+    };
+    int k = splits(kSizingSlots);
+    if (slots > 0) k = std::min(k, splits(slots));
     c.chunk_tiles = (max_tiles + k - 1) / k;
     c.max_chunks = (max_tiles + c.chunk_tiles - 1) / c.chunk_tiles;
     return c;
@@ -604,7 +612,7 @@ ChunkPlan chunk_plan(int N, int Hq, int head_dim, int dtype, int total_q, int ma
 size_t prefill_mfma_workspace(int N, int Hq, int head_dim, int block_size, int dtype, int total_q,
                               int max_q_len, int max_seq_len) {
     if (!prefill_mfma_handles(head_dim, block_size, dtype) || N <= 0 || total_q <= 0) return 0;
-    const ChunkPlan c = chunk_plan(N, Hq, head_dim, dtype, total_q, max_q_len, max_seq_len);
+    const ChunkPlan c = chunk_plan(N, Hq, total_q, max_q_len, max_seq_len, 0);
     if (c.max_chunks <= 1) return 0;
     const size_t parts = (size_t)N * c.qblocks * c.max_chunks * Hq;
     return parts * BQ * sizeof(float) + parts * BQ * head_dim * sizeof(float);
@@ -615,17 +623,20 @@ int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dty
                         size_t workspace_bytes, hipStream_t st) {
     if (!prefill_mfma_handles(head_dim, block_size, dtype)) return -1;
     if (((uintptr_t)a.q | (uintptr_t)a.out | (uintptr_t)a.k | (uintptr_t)a.v) & 15) return -1;
-    const ChunkPlan c = chunk_plan(a.N, a.Hq, head_dim, dtype, total_q, max_q_len, max_seq_len);
+    const int slots = resident_workgroups(prefill_kernel_fn(dtype, head_dim), 256);
+    const ChunkPlan c = chunk_plan(a.N, a.Hq, total_q, max_q_len, max_seq_len, slots);
     a.qblocks = c.qblocks;
     const size_t need = prefill_mfma_workspace(a.N, a.Hq, head_dim, block_size, dtype, total_q,
                                                max_q_len, max_seq_len);
-    if (need > 0 && workspace != nullptr && workspace_bytes >= need) {
-        const size_t parts = (size_t)a.N * c.qblocks * c.max_chunks * a.Hq;
+    if (c.max_chunks > 1 && workspace != nullptr && workspace_bytes >= need) {
+        // partials laid out for the sizing plan's chunk count (>= this plan's)
+        const ChunkPlan z = chunk_plan(a.N, a.Hq, total_q, max_q_len, max_seq_len, 0);
+        const size_t parts = (size_t)a.N * z.qblocks * z.max_chunks * a.Hq;
         a.max_chunks = c.max_chunks;
         a.chunk_tiles = c.chunk_tiles;
         a.part_lse = reinterpret_cast<float*>(workspace);
         a.part_o = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + parts * BQ * sizeof(float));
-    } else {   // no (or too small a) workspace: one chunk per unit
+    } else {   // no split, or no (or too small a) workspace: one chunk per unit
         a.max_chunks = 1;
         a.chunk_tiles = 1 << 30;
         a.part_lse = nullptr;

@@ -108,8 +108,10 @@ def test_prefill_argument_checks():
 def test_prefill_workspace_size():
     lib = L.lib()
     ws = lib.llkv_paged_prefill_workspace_size
-    # short key ranges: no chunking, no workspace
-    assert ws(8, 4096, 512, 1000, 14, 64, 16, 1) == 0
+    # key ranges under two minimum chunks (16 tiles): no chunking, no workspace
+    assert ws(8, 4096, 512, 900, 14, 64, 16, 1) == 0
+    # enough (sequence, query block, head) units to fill the GPU unsplit: no workspace
+    assert ws(64, 32768, 512, 4608, 14, 64, 16, 1) == 0
     # configuration 4 (keys up to 4608): chunked, fp32 partials of 128 rows x (D + 1)
     n = ws(8, 4096, 512, 4608, 14, 64, 16, 1)
     assert n > 0 and n % (128 * 65 * 4) == 0

@@ -380,11 +380,16 @@ PREFILL = [
     ("bf16_D64", 14, 2, 64, [16, 200], [100, 256], torch.bfloat16, True),
     ("bf16_D128", 32, 8, 128, [64], [200], torch.bfloat16, True),
     ("fp16_mha", 4, 4, 64, [31], [97], torch.float16, True),
-    # key ranges over 16 tiles (1024 keys): run as parallel chunks + merge
+    # long key ranges of a small batch: run as parallel key chunks + merge
     ("fp16_D64_long_noncausal", 14, 2, 64, [3000], [100], torch.float16, False),
     ("bf16_D64_long", 14, 2, 64, [2500, 0], [300, 40], torch.bfloat16, True),
     ("fp16_D128_long", 32, 8, 128, [2100], [130], torch.float16, True),
 ]
+
+
+# many (sequence, query block, head) units: the key ranges run unsplit
+PREFILL.append(("fp16_D64_many_units", 14, 2, 64, [(37 * i) % 700 for i in range(48)], [256] * 48,
+                torch.float16, True))
 
 
 @pytest.mark.parametrize("name,hq,hkv,d,prefixes,chunks,dtype,causal", PREFILL,
@@ -400,6 +405,26 @@ def test_prefill_cases(name, hq, hkv, d, prefixes, chunks, dtype, causal):
         check_fp32(out, ref, name)
     else:
         check_lowp(out, ref, name, 2e-3 if dtype == torch.float16 else 1.6e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_loose_bounds(dtype):
+    """Host bounds far above the actual lengths (more key chunks and query blocks planned than
+    the sequences use): the extra work-groups find nothing to do and the result is unchanged."""
+    say(f"prefill with loose max_q_len / max_seq_len bounds {dtype}")
+    prefixes, chunks = [900, 0, 2000], [64, 300, 129]
+    nb = sum((p + c + 15) // 16 for p, c in zip(prefixes, chunks)) + 4
+    case = wl.prefill_case("loose", 14, 2, 64, prefixes, chunks, {}, nb, dtype, seed=77)
+    kp, vp = case.k_pool.to(DEV), case.v_pool.to(DEV)
+    kc.append_kv(case.k_chunk.to(DEV), case.v_chunk.to(DEV), case.slots.to(DEV), kp, vp)
+    args = (case.q.to(DEV), kp, vp, case.block_table.to(DEV), case.cu_q.to(DEV), case.seq_lens.to(DEV))
+    tight = kc.paged_prefill(*args, case.max_q_len, case.max_seq_len, causal=True, scale=case.scale)
+    loose = kc.paged_prefill(*args, 4 * case.max_q_len, 8 * case.max_seq_len, causal=True,
+                             scale=case.scale)
+    torch.cuda.synchronize()
+    ref = oracle_prefill(case, kp, vp)
+    check_lowp(loose, ref, "prefill loose bounds", 2e-3 if dtype == torch.float16 else 1.6e-2)
+    check_lowp(tight, ref, "prefill tight bounds", 2e-3 if dtype == torch.float16 else 1.6e-2)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
