@@ -97,6 +97,48 @@ int llkv_gather(void* k_dst, void* v_dst, const void* k_pool,
                 void* stream);
 
 /* ------------------------------------------------------------------------
+ * Device-side step metadata and fused RoPE + KV append (the next rows of the
+ * path: the engine's per-token host loops and memcpys, and its separate RoPE
+ * pass, become two launches per layer).
+ * ------------------------------------------------------------------------ */
+
+/* Slot mapping built on the device.  Replaces the host loops of
+ * EngineServer::scatter_prefill_kv (src/engine/engine_server.cpp:731-757) and
+ * write_decode_kv (:760-787), which look up phys = block_table[pos / bs] and
+ * offset = pos % bs per token and issue two cudaMemcpy each.  Token t of
+ * sequence n (rows cu_tokens[n] .. cu_tokens[n+1]-1) sits at position
+ * start_pos[n] + (t - cu_tokens[n]); slots[t] = phys * bs + pos % bs, or -1
+ * when the position lies outside the table or on a -1 entry (the reference
+ * skips such a write, :766-774).  A decode step is cu_tokens = 0..B,
+ * start_pos = seq_lens.  block_table: device int32 [num_seqs, max_blocks];
+ * cu_tokens: device int32 [num_seqs + 1]; start_pos: device int32 [num_seqs];
+ * slots: device int64 [num_tokens]. */
+int llkv_build_slots(int64_t* slots, const int* block_table, int max_blocks,
+                     const int* cu_tokens, const int* start_pos, int num_seqs,
+                     int num_tokens, int block_size, void* stream);
+
+/* Fused RoPE + KV append.  Replaces lightllm::ops::rope
+ * (include/lightllm/ops/rope.h:8-13, src/ops/rope.cu:29-92) on q and k,
+ * followed by write_decode_kv / scatter_prefill_kv.  Neox rotation of the first
+ * rotary_dim dims of every head, pairs (i, i + rotary_dim/2):
+ *     x1' = x1 * cos[t][i] - x2 * sin[t][i]
+ *     x2' = x2 * cos[t][i] + x1 * sin[t][i]
+ * in fp32 with each product and the sum rounded separately (no fused
+ * multiply-add), then rounded to the element type.  Dims >= rotary_dim are
+ * unchanged.  q [num_tokens, Hq, D] (may be NULL) and k [num_tokens, Hkv, D]
+ * are rotated in place; the rotated k row and the v row are then written to
+ * pool row slot_mapping[t] (negative = no pool write).  cos, sin: device fp32
+ * [num_tokens, rotary_dim / 2], as the reference builds them
+ * (engine_server.cpp:1553-1585).  rotary_dim even, 2 <= rotary_dim <= D.
+ * The reference kernel's indexing rotates a single pair per (token, head)
+ * when its block has more than one thread (rope.cu:41-53 with the launch of
+ * :69-74); this entry point applies the rotation the header documents. */
+int llkv_rope_append(void* q, void* k, const void* v, void* k_pool, void* v_pool,
+                     const int64_t* slot_mapping, const float* cos, const float* sin,
+                     int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                     int rotary_dim, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
  * Paged decode attention (one new token per sequence), with Split-K.
  * Replaces lightllm::kv_cache::paged_attention
  * (include/lightllm/kv_cache/paged_attention.h:31-36,
@@ -108,17 +150,19 @@ int llkv_gather(void* k_dst, void* v_dst, const void* k_pool,
  * seq_lens   : device int32 [num_seqs]; sequence b attends positions [0, len).
  * max_seq_len: host-side upper bound of every seq_lens[b] (sizes the grid
  *              without the reference's device-to-host read).
- * num_splits : 0 = automatic: the batch's pages are shared equally among as
- *              many work-groups as the GPU holds at once, whatever the length
- *              mix (up to 1024 sequences; larger batches use 8-page splits);
+ * num_splits : 0 = automatic, chosen from the kernel's resident work-group
+ *              count: with few (sequence, kv head) units each is cut into
+ *              S ~ 0.8 x resident / units fixed splits; with many (up to 1024
+ *              sequences) the batch's pages are shared equally among one
+ *              resident set of work-groups, whatever the length mix (larger
+ *              batches use 8-page splits);
  *              S > 0 = the reference's fixed split (S ranges of ceil(n/S) pages).
  * scale      : softmax scale (the reference uses 1/sqrt(head_dim)).
  * workspace  : device memory of at least llkv_paged_decode_workspace_size()
  *              bytes (may be NULL when that size is 0); it holds the split
- *              partials and arrival counters.  It must be zero-filled before
- *              its first use; every call leaves the counters zero again, so
- *              one workspace serves any later call.  Calls sharing one
- *              workspace must not overlap.
+ *              partials (and the balanced schedule's page prefix sums), all
+ *              written before they are read within one call, so it needs no
+ *              initialisation.  Calls sharing one workspace must not overlap.
  * ------------------------------------------------------------------------ */
 size_t llkv_paged_decode_workspace_size(int num_seqs, int num_q_heads,
                                         int num_kv_heads, int head_dim,

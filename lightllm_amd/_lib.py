@@ -40,6 +40,9 @@ _SIGS = {
                                              c_int, c_int, c_int, c_int, c_void_p]),
     "llkv_gather": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int,
                             c_int64, c_int, c_int, c_int, c_int, c_void_p]),
+    "llkv_build_slots": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int, c_int,
+                                 c_void_p]),
+    "llkv_rope_append": (c_int, [c_void_p] * 8 + [c_int] * 6 + [c_void_p]),
     "llkv_paged_decode_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "llkv_paged_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                   c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int,

@@ -158,6 +158,43 @@ def append_kv(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
                             k.shape[0], hkv, d, dtype_code(k_pool.dtype), _stream(stream)))
 
 
+def build_slots(block_table: torch.Tensor, cu_tokens: torch.Tensor, start_pos: torch.Tensor,
+                num_tokens: int, block_size: int = 16, out: Optional[torch.Tensor] = None,
+                stream=None) -> torch.Tensor:
+    """Device slot mapping: token t of sequence n (rows cu_tokens[n]..) sits at position
+    start_pos[n] + t - cu_tokens[n]; slot = table[n][pos // bs] * bs + pos % bs, or -1 outside
+    the table (the reference's write_decode_kv / scatter_prefill_kv host loops)."""
+    for name, t in (("block_table", block_table), ("cu_tokens", cu_tokens), ("start_pos", start_pos)):
+        _require(t, torch.int32, name)
+    if out is None:
+        out = torch.empty(num_tokens, dtype=torch.int64, device=block_table.device)
+    _require(out, torch.int64, "out")
+    check(lib().llkv_build_slots(_ptr(out), _ptr(block_table), block_table.shape[1], _ptr(cu_tokens),
+                                 _ptr(start_pos), start_pos.shape[0], num_tokens, block_size,
+                                 _stream(stream)))
+    return out
+
+
+def rope_append(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
+                cos: torch.Tensor, sin: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                stream=None) -> None:
+    """Fused RoPE + KV append: q [T, Hq, D] (or None) and k [T, Hkv, D] rotated in place over the
+    first 2 * cos.shape[1] dims (Neox halves), then the k and v rows written to pool rows
+    slot_mapping[t] (<0 skips).  cos / sin: fp32 [T, rotary_dim / 2]."""
+    _require(slot_mapping, torch.int64, "slot_mapping")
+    _require(k, k_pool.dtype, "k")
+    _require(v, k_pool.dtype, "v")
+    if q is not None:
+        _require(q, k_pool.dtype, "q")
+    _require(cos, torch.float32, "cos")
+    _require(sin, torch.float32, "sin")
+    t, hkv, d = k.shape
+    hq = q.shape[1] if q is not None else 0
+    check(lib().llkv_rope_append(_ptr(q), _ptr(k), _ptr(v), _ptr(k_pool), _ptr(v_pool),
+                                 _ptr(slot_mapping), _ptr(cos), _ptr(sin), t, hq, hkv, d,
+                                 2 * cos.shape[1], dtype_code(k_pool.dtype), _stream(stream)))
+
+
 def scatter_prefill_kv(k: torch.Tensor, v: torch.Tensor, start_pos: int, n_tokens: int,
                        block_table: torch.Tensor, max_blocks: int, allocator: BlockAllocator,
                        stream=None) -> None:

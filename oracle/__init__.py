@@ -105,6 +105,31 @@ def append_slots(k_pool: np.ndarray, v_pool: np.ndarray, k_src, v_src, slots) ->
                            c_int64(slots.size), hkv, d, k_pool.itemsize)
 
 
+def build_slots(block_table, cu, start_pos, num_tokens: int, block_size: int = 16) -> np.ndarray:
+    """Slot mapping of a step (-1 outside the table)."""
+    bt = _i32(block_table)
+    cu, start = _i32(cu), _i32(start_pos)
+    out = np.full(num_tokens, -7, dtype=np.int64)
+    lib().llo_build_slots(_p(out), _p(bt), bt.shape[1], _p(cu), _p(start), start.size, num_tokens,
+                          block_size)
+    return out
+
+
+def rope_append(q, k, v, k_pool, v_pool, slots, cos, sin, dtype: int) -> None:
+    """In place: RoPE on q (or None) and k, then k / v rows appended at slots.  Arrays hold fp32
+    values (dtype 0) or fp16 / bf16 bit patterns as uint16 (dtype 1 / 2), contiguous."""
+    want = np.float32 if dtype == 0 else np.uint16
+    for a in (q, k, v, k_pool, v_pool):
+        if a is not None:
+            assert a.dtype == want and a.flags.c_contiguous
+    cos, sin = _f32(cos), _f32(sin)
+    slots = np.ascontiguousarray(slots, dtype=np.int64)
+    t, hkv, d = k.shape
+    hq = q.shape[1] if q is not None else 0
+    lib().llo_rope_append(_p(q) if q is not None else None, _p(k), _p(v), _p(k_pool), _p(v_pool),
+                          _p(slots), _p(cos), _p(sin), t, hq, hkv, d, 2 * cos.shape[1], dtype)
+
+
 def scatter_prefill(k_pool, v_pool, k_src, v_src, start_pos: int, n_tokens: int, table) -> None:
     nb, bs, hkv, d = k_pool.shape
     k_src = np.ascontiguousarray(k_src, dtype=k_pool.dtype)

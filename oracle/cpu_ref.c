@@ -128,6 +128,78 @@ void llo_append_slots(void* k_pool, void* v_pool, const void* k_src,
     }
 }
 
+/* Slot mapping of a step.  Restates the host loops of
+ * EngineServer::scatter_prefill_kv (src/engine/engine_server.cpp:731-757) and
+ * write_decode_kv (:760-787): pos = start + i, phys = table[pos / bs],
+ * row = phys*bs + pos%bs; a position outside the table is skipped
+ * (:766-774), here slot -1.  Token t belongs to the sequence n with
+ * cu[n] <= t < cu[n+1]. */
+void llo_build_slots(int64_t* slots, const int* block_table, int max_blocks,
+                     const int* cu, const int* start_pos, int n, int num_tokens,
+                     int block_size) {
+    for (int e = 0; e < n; e++) {
+        for (int t = cu[e]; t < cu[e + 1] && t < num_tokens; t++) {
+            int pos = start_pos[e] + (t - cu[e]);
+            int64_t slot = -1;
+            if (pos >= 0 && pos / block_size < max_blocks) {
+                int phys = block_table[(size_t)e * max_blocks + pos / block_size];
+                if (phys >= 0) slot = (int64_t)phys * block_size + pos % block_size;
+            }
+            slots[t] = slot;
+        }
+    }
+}
+
+static float load_elem(const void* p, size_t i, int dtype) {
+    if (dtype == 0) return ((const float*)p)[i];
+    if (dtype == 1) return llo_f16_to_f32(((const uint16_t*)p)[i]);
+    return llo_bf16_to_f32(((const uint16_t*)p)[i]);
+}
+
+static void store_elem(void* p, size_t i, int dtype, float x) {
+    if (dtype == 0) ((float*)p)[i] = x;
+    else if (dtype == 1) ((uint16_t*)p)[i] = llo_f32_to_f16(x);
+    else ((uint16_t*)p)[i] = llo_f32_to_bf16(x);
+}
+
+/* One Neox pair: the arithmetic of src/ops/rope.cu:54-57 with every product
+ * and sum rounded to fp32 on its own (no contraction into fused
+ * multiply-adds, which -march=x86-64-v3 would otherwise allow). */
+__attribute__((optimize("fp-contract=off"), noinline))
+static void rope_pair(float x1, float x2, float c, float s, float* o1, float* o2) {
+    float a = x1 * c, b = x2 * s, d = x2 * c, e = x1 * s;
+    *o1 = a - b;
+    *o2 = d + e;
+}
+
+static void rope_rows(void* x, int T, int H, int D, int half, const float* cos,
+                      const float* sin, int dtype) {
+    for (int t = 0; t < T; t++)
+        for (int h = 0; h < H; h++) {
+            size_t row = ((size_t)t * H + h) * D;
+            for (int i = 0; i < half; i++) {
+                float o1, o2;
+                rope_pair(load_elem(x, row + i, dtype), load_elem(x, row + half + i, dtype),
+                          cos[(size_t)t * half + i], sin[(size_t)t * half + i], &o1, &o2);
+                store_elem(x, row + i, dtype, o1);
+                store_elem(x, row + half + i, dtype, o2);
+            }
+        }
+}
+
+/* RoPE on q and k (the documented contract of include/lightllm/ops/rope.h:8-13:
+ * Neox halves of the first rotary_dim dims, cos/sin [T, rotary_dim/2]), then the
+ * rotated k rows and the v rows appended at slot_mapping (llo_append_slots).
+ * q may be NULL.  dtype: 0 fp32, 1 fp16, 2 bf16. */
+void llo_rope_append(void* q, void* k, const void* v, void* k_pool, void* v_pool,
+                     const int64_t* slot_mapping, const float* cos, const float* sin,
+                     int T, int Hq, int Hkv, int D, int rotary_dim, int dtype) {
+    int half = rotary_dim / 2;
+    if (q) rope_rows(q, T, Hq, D, half, cos, sin, dtype);
+    rope_rows(k, T, Hkv, D, half, cos, sin, dtype);
+    llo_append_slots(k_pool, v_pool, k, v, slot_mapping, T, Hkv, D, dtype == 0 ? 4 : 2);
+}
+
 /* src/kv_cache/paged_attention.cu:986-1010 (scatter_prefill_kv_kernel):
  * token t of the chunk goes to pos = start_pos + t, phys = bt[pos/bs], offset pos%bs. */
 void llo_scatter_prefill(void* k_pool, void* v_pool, const void* k_src,

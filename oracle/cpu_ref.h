@@ -33,6 +33,13 @@
  *   llo_paged_prefill[_f64]               numpy per-sequence gather + masked softmax
  *   llo_first_prefill_batched             numpy per-entry causal softmax
  *   llo_fnv1a_tokens                      published FNV-1a 64 vectors ("", "a", "abc")
+ *   llo_build_slots                       pure-Python position walk; decode form (cu = 0..B,
+ *                                         start = lengths) equals table[len/16]*16 + len%16
+ *   llo_rope_append                       numpy float32 rotation (separately rounded products
+ *                                         and sums), bit-exact for fp32 / fp16 / bf16; the
+ *                                         reference's own rope known answer (tests/test_ops.cu:51-61);
+ *                                         rotation by angle 0 is the identity, cos/sin of a
+ *                                         true angle preserve each pair's norm
  * No function is left unpinned.
  */
 #ifndef LIGHTLLM_ORACLE_CPU_REF_H
@@ -74,6 +81,12 @@ void llo_scatter_prefill_batched(void* k_pool, void* v_pool,
                                  const int* token_cumsum, const int* flat_bt,
                                  int max_blocks, int N, int block_size,
                                  int elem_size);
+void llo_build_slots(int64_t* slots, const int* block_table, int max_blocks,
+                     const int* cu, const int* start_pos, int n, int num_tokens,
+                     int block_size);
+void llo_rope_append(void* q, void* k, const void* v, void* k_pool, void* v_pool,
+                     const int64_t* slot_mapping, const float* cos, const float* sin,
+                     int T, int Hq, int Hkv, int D, int rotary_dim, int dtype);
 void llo_reconstruct_kv(void* k_out, void* v_out, const void* k_pool,
                         const void* v_pool, const int* block_table,
                         int seq_len, int block_size, int Hkv, int D,

@@ -40,7 +40,7 @@ def test_python_bindings_cover_the_header():
 
 def test_version_and_status_strings():
     lib = L.lib()
-    assert lib.llkv_abi_version() == 2
+    assert lib.llkv_abi_version() == 3
     assert L.status_string(0) == "ok"
     assert "invalid" in L.status_string(1)
     assert "unsupported" in L.status_string(2) or "support" in L.status_string(2)
@@ -103,6 +103,27 @@ def test_prefill_argument_checks():
     rc, msg = _err(lib.llkv_paged_prefill(None, None, None, None, None, 8, None, None, 1, 16, 16,
                                           16, 14, 2, 512, 16, 1, 0.1, 0, None, 0, None))
     assert rc == 2 and "256" in msg
+
+
+def test_rope_append_argument_checks():
+    lib = L.lib()
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: the checks fail first
+    rc, msg = _err(lib.llkv_rope_append(fake, fake, fake, fake, fake, fake, fake, fake, 4, 8, 2, 64,
+                                        63, 1, None))
+    assert rc == 1 and "rotary_dim" in msg
+    rc, msg = _err(lib.llkv_rope_append(fake, fake, fake, fake, fake, fake, fake, fake, 4, 8, 2, 64,
+                                        80, 1, None))
+    assert rc == 1 and "rotary_dim" in msg
+    rc, msg = _err(lib.llkv_rope_append(None, None, fake, fake, fake, fake, fake, fake, 4, 8, 2, 64,
+                                        64, 1, None))
+    assert rc == 1 and "null" in msg
+    rc, msg = _err(lib.llkv_rope_append(fake, fake, fake, fake, fake, fake, fake, fake, 4, 8, 2, 64,
+                                        64, 7, None))
+    assert rc == 1 and "dtype" in msg
+    assert lib.llkv_rope_append(None, None, None, None, None, None, None, None, 0, 8, 2, 64, 64, 1,
+                                None) == 0   # nothing to do
+    rc, msg = _err(lib.llkv_build_slots(None, None, 4, None, None, 2, 5, 16, None))
+    assert rc == 1 and "null" in msg
 
 
 def test_prefill_workspace_size():

@@ -91,6 +91,125 @@ def test_append_bit_exact(dtype):
     assert np.array_equal(bits(kd), ke) and np.array_equal(bits(vd), ve)
 
 
+def _host_arr(t: torch.Tensor) -> np.ndarray:
+    """fp32 values, or fp16 / bf16 bit patterns as uint16 (the oracle's rope_append input)."""
+    if t.dtype == torch.float32:
+        return t.detach().cpu().contiguous().numpy().copy()
+    return bits(t).view(np.uint16).copy()
+
+
+def test_build_slots_matches_oracle():
+    say("build_slots: prefill chunks and a decode step")
+    g = torch.Generator().manual_seed(21)
+    n, mb = 9, 40
+    table = torch.randperm(4096, generator=g)[: n * mb].reshape(n, mb).to(torch.int32)
+    table[2, 10:] = -1
+    counts = [1, 300, 0, 17, 64, 1, 129, 2, 5]
+    cu = torch.tensor([0] + list(np.cumsum(counts)), dtype=torch.int32)
+    start = torch.tensor([0, 100, 3, 600, 0, 639, 500, 200, 636], dtype=torch.int32)
+    T = int(cu[-1])
+    got = kc.build_slots(table.to(DEV), cu.to(DEV), start.to(DEV), T)
+    want = oracle.build_slots(table.numpy(), cu.numpy(), start.numpy(), T)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), want)
+    assert (want == -1).any()
+    lens = torch.randint(0, mb * 16, (n,), generator=g, dtype=torch.int32)
+    dec = kc.build_slots(table.to(DEV), torch.arange(n + 1, dtype=torch.int32, device=DEV), lens.to(DEV), n)
+    assert np.array_equal(dec.cpu().numpy(), oracle.build_slots(table.numpy(), np.arange(n + 1), lens.numpy(), n))
+
+
+ROPE_CASES = [
+    # (name, T, Hq, Hkv, D, rotary_dim, dtype, q present, pointer offset (elements))
+    ("f32_full", 37, 14, 2, 64, 64, torch.float32, True, 0),
+    ("f32_partial", 37, 14, 2, 64, 32, torch.float32, True, 0),
+    ("f16_llama", 300, 32, 8, 128, 128, torch.float16, True, 0),
+    ("bf16_llama", 300, 32, 8, 128, 128, torch.bfloat16, True, 0),
+    ("f16_k_only", 64, 0, 8, 128, 64, torch.float16, False, 0),
+    ("f16_scalar_rot36", 19, 4, 2, 64, 36, torch.float16, True, 0),    # half % 8 != 0: scalar path
+    ("f32_scalar_unaligned", 23, 6, 2, 64, 64, torch.float32, True, 1),  # 4-byte offset rows
+]
+
+
+@pytest.mark.parametrize("name,T,hq,hkv,d,rot,dtype,with_q,off", ROPE_CASES,
+                         ids=[c[0] for c in ROPE_CASES])
+def test_rope_append_bit_exact(name, T, hq, hkv, d, rot, dtype, with_q, off):
+    """Fused RoPE + append: q, k rotated in place and the pool rows, bit for bit the oracle's
+    (both round every product and sum separately)."""
+    say(f"rope_append {name}")
+    g = torch.Generator().manual_seed(len(name))
+    nb = (T + 15) // 16 + 8
+    q = torch.randn(T, hq, d, generator=g).to(dtype) if with_q else None
+    k = torch.randn(T, hkv, d, generator=g).to(dtype)
+    v = torch.randn(T, hkv, d, generator=g).to(dtype)
+    pos = torch.randint(0, 20000, (T,), generator=g).double()
+    inv = 1.0 / (500000.0 ** (torch.arange(rot // 2).double() * 2.0 / rot))
+    ang = pos[:, None] * inv[None, :]
+    cos, sin = torch.cos(ang).float(), torch.sin(ang).float()
+    slots = torch.randperm(nb * 16, generator=g)[:T].to(torch.int64)
+    slots[::7] = -1
+    kp = torch.randn(nb, 16, hkv, d, generator=g).to(dtype)
+    vp = torch.randn(nb, 16, hkv, d, generator=g).to(dtype)
+
+    def dev(t):   # device copy, optionally at an element offset (unaligned rows)
+        if t is None:
+            return None
+        buf = torch.empty(t.numel() + off, dtype=t.dtype, device=DEV)
+        view = buf[off:].view(t.shape)
+        view.copy_(t.to(DEV))
+        return view
+
+    qd, kd, vd, kpd, vpd = dev(q), dev(k), dev(v), dev(kp), dev(vp)
+    kc.rope_append(qd, kd, vd, slots.to(DEV), cos.to(DEV), sin.to(DEV), kpd, vpd)
+    torch.cuda.synchronize()
+    code = dtype_code(dtype)
+    qh = _host_arr(q) if with_q else None
+    kh, vh, kph, vph = _host_arr(k), _host_arr(v), _host_arr(kp), _host_arr(vp)
+    oracle.rope_append(qh, kh, vh, kph, vph, slots.numpy(), cos.numpy(), sin.numpy(), code)
+    if with_q:
+        assert np.array_equal(_host_arr(qd).view(np.uint8), qh.view(np.uint8)), "q"
+    assert np.array_equal(_host_arr(kd).view(np.uint8), kh.view(np.uint8)), "k"
+    assert np.array_equal(_host_arr(kpd).view(np.uint8), kph.view(np.uint8)), "k pool"
+    assert np.array_equal(_host_arr(vpd).view(np.uint8), vph.view(np.uint8)), "v pool"
+
+
+def test_rope_append_step_with_device_slots_then_decode():
+    """A decode step the engine way: slots built on the device from the table and lengths, RoPE +
+    append in one launch, then paged decode over the appended token."""
+    say("rope_append + build_slots + decode (B=64, 32/8/128 fp16)")
+    g = torch.Generator().manual_seed(33)
+    B, hq, hkv, d, nb = 64, 32, 8, 128, 4096
+    lens = torch.randint(1, 900, (B,), generator=g, dtype=torch.int32)
+    mb = (int(lens.max()) + 1 + 15) // 16
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    table, _ = wl._tables([int(L) + 1 for L in lens], perm, mb)
+    kp, vp = wl.device_pools(nb, hkv, d, torch.float16, 34, DEV)
+    q = torch.randn(B, hq, d, generator=g).to(torch.float16)
+    k = torch.randn(B, hkv, d, generator=g).to(torch.float16)
+    v = torch.randn(B, hkv, d, generator=g).to(torch.float16)
+    inv = 1.0 / (500000.0 ** (torch.arange(d // 2).double() * 2.0 / d))
+    ang = lens.double()[:, None] * inv[None, :]
+    cos, sin = torch.cos(ang).float(), torch.sin(ang).float()
+    kp0, vp0 = kp.clone(), vp.clone()
+    td, qd, kd = table.to(DEV), q.to(DEV), k.to(DEV)
+    slots = kc.build_slots(td, torch.arange(B + 1, dtype=torch.int32, device=DEV), lens.to(DEV), B)
+    kc.rope_append(qd, kd, v.to(DEV), slots, cos.to(DEV), sin.to(DEV), kp, vp)
+    out = kc.paged_decode(qd, kp, vp, td, (lens + 1).to(DEV), int(lens.max()) + 1)
+    torch.cuda.synchronize()
+    # oracle: the same three steps on the host
+    sl = oracle.build_slots(table.numpy(), np.arange(B + 1), lens.numpy(), B)
+    assert np.array_equal(slots.cpu().numpy(), sl)
+    qh, kh, vh = _host_arr(q), _host_arr(k), _host_arr(v)
+    kph, vph = _host_arr(kp0), _host_arr(vp0)
+    oracle.rope_append(qh, kh, vh, kph, vph, sl, cos.numpy(), sin.numpy(), 1)
+    assert np.array_equal(_host_arr(kp).view(np.uint8), kph.view(np.uint8))
+    assert np.array_equal(_host_arr(vp).view(np.uint8), vph.view(np.uint8))
+    assert np.array_equal(_host_arr(qd).view(np.uint8), qh.view(np.uint8))
+    f = lambda b: torch.from_numpy(b.view(np.int16)).view(torch.float16).float().numpy()
+    ref = oracle.paged_decode(f(qh), f(kph), f(vph), table.numpy(), (lens + 1).numpy(), f64=True,
+                              nthreads=16)
+    check_lowp(out, ref, "decode after rope_append", 2e-3)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_scatter_and_gather_round_trip(dtype):
     say(f"scatter/gather dtype={dtype}")

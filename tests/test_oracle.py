@@ -423,3 +423,134 @@ def test_first_prefill_batched_matches_numpy():
             ref = np_attend(q[cum[e] + r], k[cum[e]:cum[e + 1]], v[cum[e]:cum[e + 1]], 0.3,
                             [r + 1] * hq)
             close(out[cum[e] + r], ref, 1e-5, 1e-6)
+
+
+# ---------------------------------------------------------------------------
+# step metadata and fused RoPE + append
+# ---------------------------------------------------------------------------
+
+def py_slots(table, cu, start, bs=PAGE):
+    """Pure-Python walk of the reference's host loops (engine_server.cpp:731-787)."""
+    out = []
+    for e in range(len(start)):
+        for i in range(cu[e + 1] - cu[e]):
+            pos = start[e] + i
+            blk = pos // bs
+            if pos < 0 or blk >= table.shape[1] or table[e, blk] < 0:
+                out.append(-1)
+            else:
+                out.append(int(table[e, blk]) * bs + pos % bs)
+    return np.array(out, dtype=np.int64)
+
+
+def test_build_slots_matches_python_walk():
+    rng = np.random.default_rng(3)
+    n, mb = 6, 5
+    table = rng.permutation(200)[: n * mb].reshape(n, mb).astype(np.int32)
+    table[1, 3:] = -1
+    table[4, 0] = -1
+    counts = np.array([1, 17, 0, 40, 3, 9])
+    cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    start = np.array([0, 30, 5, 50, 0, 70], dtype=np.int32)   # seq 5 runs past the table
+    got = oracle.build_slots(table, cu, start, int(cu[-1]))
+    assert np.array_equal(got, py_slots(table, cu, start))
+    assert (got == -1).any() and (got >= 0).any()
+    # decode form: one token per sequence at its current length
+    lens = np.array([0, 15, 16, 63, 64, 79], dtype=np.int32)
+    dec = oracle.build_slots(table, np.arange(n + 1, dtype=np.int32), lens, n)
+    for b in range(n):
+        want = table[b, lens[b] // PAGE] * PAGE + lens[b] % PAGE if lens[b] // PAGE < mb else -1
+        want = -1 if lens[b] // PAGE < mb and table[b, lens[b] // PAGE] < 0 else want
+        assert dec[b] == want
+
+
+def np_rope_f32(x, cos, sin):
+    """float32 Neox rotation with separately rounded products and sums (numpy float32 ops)."""
+    half = cos.shape[1]
+    x = x.astype(np.float32).copy()
+    x1, x2 = x[..., :half].copy(), x[..., half:2 * half].copy()
+    c, s = cos[:, None, :], sin[:, None, :]
+    x[..., :half] = (x1 * c) - (x2 * s)
+    x[..., half:2 * half] = (x2 * c) + (x1 * s)
+    return x
+
+
+def _to_bits(x32, dtype):
+    if dtype == 1:
+        return x32.astype(np.float16).view(np.uint16)
+    return torch.from_numpy(x32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def _from_bits(b, dtype):
+    if dtype == 1:
+        return b.view(np.float16).astype(np.float32)
+    return torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).float().numpy()
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+@pytest.mark.parametrize("rot", [64, 32])
+def test_rope_append_matches_numpy(dtype, rot):
+    rng = np.random.default_rng(10 + dtype)
+    T, hq, hkv, d, nb = 7, 6, 2, 64, 12
+    q32 = rng.standard_normal((T, hq, d)).astype(np.float32)
+    k32 = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    v32 = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    pos = rng.integers(0, 5000, T)
+    inv = 1.0 / (10000.0 ** (np.arange(rot // 2) * 2.0 / rot))
+    ang = (pos[:, None] * inv[None, :]).astype(np.float32)
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    slots = np.array([3, -1, 17, 40, 0, 191, 100], dtype=np.int64)
+    if dtype == 0:
+        q, k, v = q32.copy(), k32.copy(), v32.copy()
+        kp = np.zeros((nb, PAGE, hkv, d), np.float32)
+    else:
+        q, k, v = _to_bits(q32, dtype), _to_bits(k32, dtype), _to_bits(v32, dtype)
+        kp = np.zeros((nb, PAGE, hkv, d), np.uint16)
+    vp = kp.copy()
+    qin, kin = q.copy(), k.copy()
+    oracle.rope_append(q, k, v, kp, vp, slots, cos, sin, dtype)
+    if dtype == 0:
+        want_q, want_k = np_rope_f32(qin, cos, sin), np_rope_f32(kin, cos, sin)
+    else:
+        want_q = _to_bits(np_rope_f32(_from_bits(qin, dtype), cos, sin), dtype)
+        want_k = _to_bits(np_rope_f32(_from_bits(kin, dtype), cos, sin), dtype)
+    assert np.array_equal(q.view(np.uint32 if dtype == 0 else np.uint16),
+                          want_q.view(np.uint32 if dtype == 0 else np.uint16))
+    assert np.array_equal(k.view(np.uint32 if dtype == 0 else np.uint16),
+                          want_k.view(np.uint32 if dtype == 0 else np.uint16))
+    if rot < d:   # dims past rotary_dim untouched
+        assert np.array_equal(q[..., rot:], qin[..., rot:])
+    kr, vr = kp.reshape(-1, hkv, d), vp.reshape(-1, hkv, d)
+    for t, s in enumerate(slots):
+        if s < 0:
+            continue
+        assert np.array_equal(kr[s], k[t]) and np.array_equal(vr[s], v[t])
+    written = set(int(s) for s in slots if s >= 0)
+    untouched = [r for r in range(nb * PAGE) if r not in written]
+    assert not kr[untouched].any() and not vr[untouched].any()
+
+
+def test_rope_reference_known_answer_and_invariants():
+    # tests/test_ops.cu:51-61: T=1, H=4, D=64, q = 0.1, cos = sin = 0.5 -> x1' = 0, x2' = 0.1
+    T, H, D = 1, 4, 64
+    q = np.full((T, H, D), 0.1, np.float32)
+    k = np.zeros((T, 1, D), np.float32)
+    cos = np.full((T, D // 2), 0.5, np.float32)
+    kp = np.zeros((1, PAGE, 1, D), np.float32)
+    oracle.rope_append(q, k, k.copy(), kp, kp.copy(), np.array([-1]), cos, cos.copy(), 0)
+    assert np.all(np.abs(q[..., : D // 2]) < 0.01) and np.all(np.abs(q[..., D // 2:] - 0.1) < 0.01)
+    # angle 0 is the identity; true angles keep each pair's norm
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 2, 128)).astype(np.float32)
+    y = x.copy()
+    one, zero = np.ones((3, 64), np.float32), np.zeros((3, 64), np.float32)
+    kp = np.zeros((1, PAGE, 2, 128), np.float32)
+    oracle.rope_append(None, y, y.copy(), kp, kp.copy(), np.full(3, -1), one, zero, 0)
+    assert np.array_equal(y, x)
+    ang = rng.uniform(-50, 50, (3, 64)).astype(np.float32)
+    z = x.copy()
+    oracle.rope_append(None, z, z.copy(), kp, kp.copy(), np.full(3, -1), np.cos(ang).astype(np.float32),
+                       np.sin(ang).astype(np.float32), 0)
+    n0 = np.hypot(x[..., :64], x[..., 64:])
+    n1 = np.hypot(z[..., :64], z[..., 64:])
+    assert np.allclose(n0, n1, rtol=1e-5, atol=1e-6)
