@@ -241,7 +241,64 @@ def bench_other_configs(torch, kc, wl):
                         "decode_GBps": round(wl.decode_bytes(dec) / (dec_us * 1e-6) / 1e9, 1),
                         "prefill_us": round(pre_us, 1),
                         "prefill_mfma_frac": round(pf / (pre_us * 1e-6) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4)}
+    res["rope_append_cfg5_step"] = bench_rope_append(torch, kc, dec, pre, kp, vp, dsl_slots, pslots)
     return res
+
+
+def rope_append_bytes(T, hq, hkv, d, rot, esize):
+    """Algorithmic bytes of one llkv_rope_append call: q and k read + written in place, k and v
+    rows written to the pool, v read, cos / sin and the int64 slots read once."""
+    return (T * hq * d * esize * 2 + T * hkv * d * esize * 2 + T * hkv * d * esize * 3
+            + T * (rot // 2) * 4 * 2 + T * 8)
+
+
+def bench_rope_append(torch, kc, dec, pre, kp, vp, dec_slots, pre_slots):
+    """Fused RoPE + KV append over configuration 5's step tokens (256 decode tokens + 4 x 1024
+    prefill tokens, 32/8/128 fp16) into its 262144-page pool; HIP-graph replays.  The CPU
+    baseline is the oracle's restatement (rotate q and k, then the row copies), 1 thread."""
+    import numpy as np
+    import oracle
+    dev = torch.device("cuda:0")
+    hq, d = dec.q.shape[1], dec.q.shape[2]
+    hkv = kp.shape[2]
+    T = dec.q.shape[0] + pre.q.shape[0]
+    g = torch.Generator(device=dev).manual_seed(77)
+    q = torch.randn(T, hq, d, generator=g, device=dev).to(torch.float16)
+    k = torch.randn(T, hkv, d, generator=g, device=dev).to(torch.float16)
+    v = torch.randn(T, hkv, d, generator=g, device=dev).to(torch.float16)
+    slots = torch.cat([dec_slots, pre_slots])
+    pos = torch.cat([dec.seq_lens.double() - 1,
+                     torch.cat([torch.arange(int(L) - n, int(L)).double() for L, n in
+                                zip(pre.seq_lens.tolist(), (pre.cu_q[1:] - pre.cu_q[:-1]).tolist())])])
+    inv = 1.0 / (500000.0 ** (torch.arange(d // 2).double() * 2.0 / d))
+    ang = pos[:, None] * inv[None, :]
+    cos, sin = torch.cos(ang).float().to(dev), torch.sin(ang).float().to(dev)
+    us = _graph_us(torch, lambda i: kc.rope_append(q, k, v, slots, cos, sin, kp, vp), 20)
+    nbytes = rope_append_bytes(T, hq, hkv, d, d, 2)
+    gbps = nbytes / (us * 1e-6) / 1e9
+    # CPU baseline: the oracle on the same tokens into a host pool of the touched pages only
+    qh = q.cpu().view(torch.int16).numpy().view(np.uint16).copy()
+    kh = k.cpu().view(torch.int16).numpy().view(np.uint16).copy()
+    vh = v.cpu().view(torch.int16).numpy().view(np.uint16).copy()
+    sl = slots.cpu().numpy()
+    rows = np.unique(sl[sl >= 0])
+    remap = np.full(int(sl.max()) + 1, -1, dtype=np.int64)
+    remap[rows] = np.arange(rows.size)
+    hs = remap[sl]
+    pool = np.zeros(((rows.size + 15) // 16, 16, hkv, d), np.uint16)
+    ch, sh = cos.cpu().numpy(), sin.cpu().numpy()
+    times = []
+    for _ in range(5):
+        qq, kk = qh.copy(), kh.copy()
+        t0 = time.perf_counter()
+        oracle.rope_append(qq, kk, vh, pool, pool.copy(), hs, ch, sh, 1)
+        times.append(time.perf_counter() - t0)
+    cpu_us = statistics.median(times) * 1e6
+    return {"tokens": T, "us": round(us, 2), "bytes": nbytes, "GBps": round(gbps, 1),
+            "roofline_frac": round(gbps / HBM_PEAK_GBS, 4),
+            "cpu_baseline": {"us": round(cpu_us, 1), "GBps": round(nbytes / (cpu_us * 1e-6) / 1e9, 2),
+                             "cores": 1, "kind": "port",
+                             "sample": "the same tokens, oracle rope_append (fp16 via fp32), median of 5"}}
 
 
 def cpu_baseline(dec, budget_s: float):

@@ -15,7 +15,8 @@
 ///    (as the reference does, :555-560, :1036-1037) to size the launch; the
 ///    C ABI takes host-side bounds instead and never synchronises.
 /// Extensions (new, additive): append_kv_slots (slot-mapping append),
-/// paged_prefill_varlen (N sequences in one launch).
+/// paged_prefill_varlen (N sequences in one launch), build_slots (device slot
+/// mapping of a step) and rope_append_kv (fused RoPE + KV append).
 
 #include <cstdint>
 
@@ -69,6 +70,21 @@ void first_prefill_attn_batched_gpu_dispatch(DType dtype, void* out_ptr, const v
 /// pool row slot_mapping[i] (device int64; negative = skip).
 void append_kv_slots(const Tensor& k, const Tensor& v, const int64_t* slot_mapping,
                      BlockAllocator& allocator);
+
+/// Slot mapping of a step on the device (the per-token host loops of
+/// EngineServer::scatter_prefill_kv / write_decode_kv, engine_server.cpp:731-787):
+/// token t of sequence n (rows cu_tokens[n]..) sits at start_pos[n] + t - cu_tokens[n];
+/// slots[t] = table[n][pos / bs] * bs + pos % bs, or -1 outside the table.  All
+/// pointers are device memory; bs is the allocator's block size.
+void build_slots(int64_t* slots, const int* block_table, int max_blocks, const int* cu_tokens,
+                 const int* start_pos, int num_seqs, int num_tokens, const BlockAllocator& allocator);
+
+/// Fused RoPE + KV append: lightllm::ops::rope(q, &k, cos, sin) (ops/rope.h:8-13,
+/// Neox halves of the first 2 * cos.size(1) dims) followed by the append of the
+/// rotated k and of v at slot_mapping (device int64; negative = skip).  q may be
+/// null; q, k, v have the pool dtype; cos / sin are fp32 [T, rotary_dim / 2].
+void rope_append_kv(Tensor* q, Tensor& k, const Tensor& v, const int64_t* slot_mapping,
+                    const Tensor& cos, const Tensor& sin, BlockAllocator& allocator);
 
 /// Varlen paged prefill: q [total_q, Hq, D]; cu_q device int32 [N+1];
 /// seq_lens device int32 [N]; block_table [N, max_blocks].  Host bounds

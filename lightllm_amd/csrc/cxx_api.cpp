@@ -205,5 +205,29 @@ void append_kv_slots(const Tensor& k, const Tensor& v, const int64_t* slot_mappi
              "append_kv_slots");
 }
 
+void build_slots(int64_t* slots, const int* block_table, int max_blocks, const int* cu_tokens,
+                 const int* start_pos, int num_seqs, int num_tokens, const BlockAllocator& allocator) {
+    throw_if(llkv_build_slots(slots, block_table, max_blocks, cu_tokens, start_pos, num_seqs,
+                              num_tokens, allocator.block_size(), nullptr),
+             "build_slots");
+}
+
+void rope_append_kv(Tensor* q, Tensor& k, const Tensor& v, const int64_t* slot_mapping,
+                    const Tensor& cos, const Tensor& sin, BlockAllocator& allocator) {
+    if (q) require_pool_dtype(q->dtype(), allocator, "rope_append_kv");
+    require_pool_dtype(k.dtype(), allocator, "rope_append_kv");
+    require_pool_dtype(v.dtype(), allocator, "rope_append_kv");
+    require_device_pool(allocator, "rope_append_kv");
+    if (cos.dtype() != DType::F32 || sin.dtype() != DType::F32)
+        throw std::runtime_error("rope_append_kv: cos / sin must be fp32");
+    throw_if(llkv_rope_append(q ? q->raw() : nullptr, k.raw(), v.raw(),
+                              const_cast<void*>(allocator.k_storage_raw()),
+                              const_cast<void*>(allocator.v_storage_raw()), slot_mapping,
+                              cos.data<float>(), sin.data<float>(), k.size(0), q ? q->size(1) : 0,
+                              allocator.num_kv_heads(), allocator.head_dim(),
+                              2 * static_cast<int>(cos.size(1)), static_cast<int>(k.dtype()), nullptr),
+             "rope_append_kv");
+}
+
 }  // namespace kv_cache
 }  // namespace lightllm

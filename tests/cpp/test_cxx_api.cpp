@@ -282,11 +282,67 @@ static void test_ops_gpu() {
     CHECK("first_prefill_batched_fp32", close(g3, r3, 2e-5, 2e-6, "first_prefill_batched fp32"));
 }
 
+// Fused RoPE + append and the device slot mapping through the C++ API, bit for bit the oracle's.
+static void test_rope_append_gpu() {
+    const int Hq = 14, Hkv = 2, D = 64, bs = 16, nb = 32, T = 5;
+    BlockAllocator alloc(nb, bs, Hkv, D);
+    std::vector<int> table;
+    for (int i = 0; i < 4; ++i) table.push_back(alloc.allocate());
+    const int cu[2] = {0, T}, start[1] = {13};   // positions 13..17 cross a page boundary
+    Tensor d_bt({4}, DType::I32, Device::CUDA), d_cu({2}, DType::I32, Device::CUDA),
+        d_st({1}, DType::I32, Device::CUDA);
+    d_bt.copy_from(table.data(), 16);
+    d_cu.copy_from(cu, 8);
+    d_st.copy_from(start, 4);
+    int64_t* slots = nullptr;
+    (void)hipMalloc(&slots, T * sizeof(int64_t));
+    build_slots(slots, d_bt.data<int>(), 4, d_cu.data<int>(), d_st.data<int>(), 1, T, alloc);
+    std::vector<int64_t> got_slots(T), want_slots(T);
+    (void)hipMemcpy(got_slots.data(), slots, T * sizeof(int64_t), hipMemcpyDeviceToHost);
+    llo_build_slots(want_slots.data(), table.data(), 4, cu, start, 1, T, bs);
+    CHECK("build_slots", got_slots == want_slots);
+
+    std::vector<float> q = rnd((size_t)T * Hq * D, 31), k = rnd((size_t)T * Hkv * D, 32),
+                       v = rnd((size_t)T * Hkv * D, 33), cs((size_t)T * D / 2), sn((size_t)T * D / 2);
+    for (int t = 0; t < T; ++t)
+        for (int i = 0; i < D / 2; ++i) {
+            const double ang = (start[0] + t) / std::pow(10000.0, 2.0 * i / D);
+            cs[(size_t)t * D / 2 + i] = (float)std::cos(ang);
+            sn[(size_t)t * D / 2 + i] = (float)std::sin(ang);
+        }
+    Tensor tq({T, Hq, D}, DType::F32, Device::CUDA), tk({T, Hkv, D}, DType::F32, Device::CUDA),
+        tv({T, Hkv, D}, DType::F32, Device::CUDA), tc({T, D / 2}, DType::F32, Device::CUDA),
+        ts({T, D / 2}, DType::F32, Device::CUDA);
+    tq.copy_from(q.data(), q.size() * 4);
+    tk.copy_from(k.data(), k.size() * 4);
+    tv.copy_from(v.data(), v.size() * 4);
+    tc.copy_from(cs.data(), cs.size() * 4);
+    ts.copy_from(sn.data(), sn.size() * 4);
+    std::vector<float> kp((size_t)nb * bs * Hkv * D), vp(kp.size());
+    (void)hipMemcpy(kp.data(), alloc.k_storage_raw(), kp.size() * 4, hipMemcpyDeviceToHost);
+    (void)hipMemcpy(vp.data(), alloc.v_storage_raw(), vp.size() * 4, hipMemcpyDeviceToHost);
+    rope_append_kv(&tq, tk, tv, slots, tc, ts, alloc);
+    (void)hipDeviceSynchronize();
+    llo_rope_append(q.data(), k.data(), v.data(), kp.data(), vp.data(), want_slots.data(), cs.data(),
+                    sn.data(), T, Hq, Hkv, D, D, 0);
+    std::vector<float> gq(q.size()), gk(k.size()), gkp(kp.size()), gvp(vp.size());
+    tq.copy_to(gq.data(), gq.size() * 4);
+    tk.copy_to(gk.data(), gk.size() * 4);
+    (void)hipMemcpy(gkp.data(), alloc.k_storage_raw(), gkp.size() * 4, hipMemcpyDeviceToHost);
+    (void)hipMemcpy(gvp.data(), alloc.v_storage_raw(), gvp.size() * 4, hipMemcpyDeviceToHost);
+    CHECK("rope_append_q_bit_exact", std::memcmp(gq.data(), q.data(), q.size() * 4) == 0);
+    CHECK("rope_append_k_bit_exact", std::memcmp(gk.data(), k.data(), k.size() * 4) == 0);
+    CHECK("rope_append_pools_bit_exact", std::memcmp(gkp.data(), kp.data(), kp.size() * 4) == 0 &&
+                                             std::memcmp(gvp.data(), vp.data(), vp.size() * 4) == 0);
+    (void)hipFree(slots);
+}
+
 int main(int argc, char** argv) {
     const bool gpu = argc > 1 && std::strcmp(argv[1], "gpu") == 0;
     if (gpu) {
         std::printf("== C++ API on the GPU\n");
         test_ops_gpu();
+        test_rope_append_gpu();
     } else {
         std::printf("== BlockAllocator / BlockTable (CPU)\n");
         test_allocator_cpu();
