@@ -20,8 +20,8 @@
 // keys sits at L - P + i and sees keys <= that position.
 //
 // When the units alone would not fill the GPU, key ranges are cut into chunks
-// of chunk_tiles tiles, one work-group each (grid: (Hq, N x qblocks x
-// max_chunks)), so that a cached prefix of thousands of keys does not
+// of chunk_tiles tiles, one work-group each (N x qblocks x max_chunks x Hq
+// work-groups, the q heads of one kv head on one XCD), so that a cached prefix of thousands of keys does not
 // serialise on one work-group; their fp32 partials (normalised rows +
 // log2-sum-exp2) are merged by prefill_merge_kernel.  The split is chosen on
 // the host from the shape bounds and the kernel's resident work-group count.
@@ -44,6 +44,7 @@ struct MfmaPrefillArgs {
     int qblocks;      // query blocks per sequence
     int max_chunks;   // key chunks per (sequence, query block); grid.y = N * qblocks * max_chunks
     int chunk_tiles;  // key tiles per chunk
+    int groups;       // N * qblocks * max_chunks * Hkv (chunk slot, kv head) work items
     float* part_o;    // [N*qblocks*max_chunks*Hq][BQ][D] (max_chunks > 1)
     float* part_lse;  // [N*qblocks*max_chunks*Hq][BQ]
 };

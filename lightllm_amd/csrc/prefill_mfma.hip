@@ -118,6 +118,12 @@ __device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* orde
 
 constexpr int kPageWindow = 256;   // page ids staged in LDS at a time
 
+#ifndef LLKV_PREFILL_XCD
+#define LLKV_PREFILL_XCD 1
+#endif
+constexpr int kXcds = 8;   // XCDs of an MI355X; work-groups go to them round-robin
+
+
 template <int D>
 struct Smem {
     static constexpr int KPAD = D + 8;    // halves per K row (pad: spread LDS banks)
@@ -146,15 +152,29 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, known uniform
     const int g = lane >> 4, c16 = lane & 15;
-    // grid (Hq, ranked chunk slots): the dispatcher walks blockIdx.x fastest, so
-    // every head's work for a slot starts before the next slot's.  Work-groups
-    // run heaviest unit first: blockIdx.y / max_chunks is a rank in the
-    // descending order of the units' key tiles (longest-processing-time first,
-    // so long cached prefixes do not start last).
-    const int hq = blockIdx.x;
-    const int kvh = hq / (a.Hq / a.Hkv);
-    const int slot = blockIdx.y / a.max_chunks;
-    const int ci = blockIdx.y - slot * a.max_chunks;   // key chunk of the unit
+    // Work: Y = N x qblocks x max_chunks ranked chunk slots (blockIdx-independent
+    // order: slot / max_chunks is a rank in the descending order of the units'
+    // key tiles, longest-processing-time first) times Hkv kv-head groups of G
+    // q heads, which read the same K/V tiles.  The dispatcher hands consecutive
+    // work-groups to the 8 XCDs in turn, and each XCD has its own L2, so group
+    // j (slot-major) goes to XCD j % 8 with its G heads as that XCD's next G
+    // work-groups: they run together and share their K/V reads in one L2.
+    const int G = a.Hq / a.Hkv;
+#if LLKV_PREFILL_XCD
+    const int xcd = blockIdx.x % kXcds, r = blockIdx.x / kXcds;
+    const int j = (r / G) * kXcds + xcd;
+    if (j >= a.groups) return;
+    const int kvh = j % a.Hkv;
+    const int hq = kvh * G + r % G;
+    const int y = j / a.Hkv;
+#else
+    const int hq = blockIdx.x % a.Hq;
+    const int kvh = hq / G;
+    const int y = blockIdx.x / a.Hq;
+    if (y * a.Hkv >= a.groups) return;
+#endif
+    const int slot = y / a.max_chunks;
+    const int ci = y - slot * a.max_chunks;   // key chunk of the unit
     UnitInfo ui;
     const int unit = unit_by_rank(a, slot, sm.order, ui);  // (sequence, query block)
     const int n = unit / a.qblocks;
@@ -642,7 +662,9 @@ int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dty
         a.part_lse = nullptr;
         a.part_o = nullptr;
     }
-    dim3 grid(a.Hq, a.N * a.qblocks * a.max_chunks);
+    a.groups = a.N * a.qblocks * a.max_chunks * a.Hkv;
+    const int G = a.Hq / a.Hkv;
+    dim3 grid((unsigned)(((a.groups + kXcds - 1) / kXcds) * kXcds * G));
     dim3 mgrid(a.Hq, a.N * a.qblocks);
     const bool merge = a.max_chunks > 1;
     if (dtype == LLKV_DTYPE_F16) {
