@@ -16,7 +16,8 @@
 ///    C ABI takes host-side bounds instead and never synchronises.
 /// Extensions (new, additive): append_kv_slots (slot-mapping append),
 /// paged_prefill_varlen (N sequences in one launch), build_slots (device slot
-/// mapping of a step) and rope_append_kv (fused RoPE + KV append).
+/// mapping of a step), rope_append_kv (fused RoPE + KV append) and
+/// paged_attention_append (fused KV append + decode).
 
 #include <cstdint>
 
@@ -70,6 +71,13 @@ void first_prefill_attn_batched_gpu_dispatch(DType dtype, void* out_ptr, const v
 /// pool row slot_mapping[i] (device int64; negative = skip).
 void append_kv_slots(const Tensor& k, const Tensor& v, const int64_t* slot_mapping,
                      BlockAllocator& allocator);
+
+/// Fused KV append + decode: k_new / v_new ([T, Hkv, D], pool dtype) are appended at
+/// position seq_lens[b] - 1 of each sequence (the lengths count the new token), then
+/// decode attention as paged_attention.  Equal to the append followed by paged_attention.
+Tensor paged_attention_append(const Tensor& q, const Tensor& k_new, const Tensor& v_new,
+                              const int* block_table, int max_blocks_per_seq, const int* seq_lens,
+                              BlockAllocator& allocator);
 
 /// Slot mapping of a step on the device (the per-token host loops of
 /// EngineServer::scatter_prefill_kv / write_decode_kv, engine_server.cpp:731-787):

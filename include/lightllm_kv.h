@@ -176,6 +176,27 @@ int llkv_paged_decode(void* out, const void* q, const void* k_pool,
                       float scale, int dtype, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* Fused KV append + paged decode: llkv_append of the step's new rows followed
+ * by llkv_paged_decode, in one launch (plus the merge).  Replaces a
+ * paged_attention call (src/engine/engine_server.cpp:1812-1817) together with
+ * the per-sequence write_decode_kv loop (:1822-1854, two cudaMemcpy each); the
+ * order is append first, so the new token attends to itself (the order of a
+ * decode step in which the appended token is part of the context).
+ * k_new, v_new: [num_seqs, Hkv, D] in the pool dtype.  seq_lens already count
+ * the new token: sequence b's new row goes to position seq_lens[b] - 1
+ * (table page (L-1)/bs, row (L-1)%bs; skipped when that table entry is -1)
+ * and attention covers positions [0, seq_lens[b]).  Results equal those of
+ * the two calls made in order; the work-group that owns the new token reads
+ * it from k_new / v_new while storing it to the pools.  Other arguments as
+ * llkv_paged_decode. */
+int llkv_paged_decode_append(void* out, const void* q, const void* k_new,
+                             const void* v_new, void* k_pool, void* v_pool,
+                             const int* block_table, const int* seq_lens,
+                             int num_seqs, int num_q_heads, int num_kv_heads,
+                             int head_dim, int block_size, int max_blocks_per_seq,
+                             int max_seq_len, int num_splits, float scale, int dtype,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Paged prefill attention over cached prefixes, varlen over N sequences.
  * Generalises lightllm::kv_cache::prefill_paged_attention

@@ -27,6 +27,12 @@ struct DecodeArgs {
     // equally; plan receives the per-sequence page prefix sums [B + 1].
     int nwg;
     int* plan;
+    // Fused append (both non-null): the step's new K/V rows [B, Hkv, D].  The
+    // new token of sequence b is position len(b) - 1; the work-group whose
+    // segment holds it stores the row into the pools (k / v, written through)
+    // and reads that token from here instead of the pool.
+    const void* knew;
+    const void* vnew;
 };
 
 // Split geometry of one sequence; identical in the split and merge kernels.
@@ -77,8 +83,40 @@ constexpr float kNegBig = -1e30f;   // finite "minus infinity" for running maxim
 // cum = pages of the earlier segments of the same round.
 struct SegDesc {
     int b, kvh, pg_begin, npages, cum, tok_end, direct;
+    int new_tok;   // fused append: position of the new token if in this segment, else -1
     int64_t po_off, pl_off;
 };
+
+// Position of sequence b's new token when a fused append is on, the segment
+// [pg_begin, tok_end) holds it and the table has a page for it, else -1 (with
+// no page the append writes nothing and the decode reads the pool, as the two
+// separate calls would).
+__device__ inline int seg_new_tok(const DecodeArgs& a, int b, int pg_begin, int tok_end, int L) {
+    if (a.knew == nullptr || L <= 0 || tok_end != L || pg_begin * kPage > L - 1) return -1;
+    return a.bt[(int64_t)b * a.max_blocks + (L - 1) / kPage] >= 0 ? L - 1 : -1;
+}
+
+// Fused append: store the new K/V row of segment d's (sequence, kv head) into
+// its pool slot (skipped when the table has no page there, as llkv_append skips
+// a negative slot).  Called by every thread of the work-group.
+template <typename T, int D>
+__device__ inline void store_new_row(const DecodeArgs& a, const SegDesc& d) {
+    if (d.new_tok < 0) return;
+    const int phys = a.bt[(int64_t)d.b * a.max_blocks + d.new_tok / kPage];
+    if (phys < 0) return;
+    const int64_t dst = (((int64_t)phys * kPage + d.new_tok % kPage) * a.Hkv + d.kvh) * D;
+    const int64_t src = ((int64_t)d.b * a.Hkv + d.kvh) * D;
+    constexpr int U = D * (int)sizeof(T) / 16;   // 16-byte units per head row
+    for (int i = threadIdx.x; i < 2 * U; i += blockDim.x) {
+        const bool isv = i >= U;
+        const int u = isv ? i - U : i;
+        const uint4* from = reinterpret_cast<const uint4*>(
+                                reinterpret_cast<const T*>(isv ? a.vnew : a.knew) + src) + u;
+        uint4* to = reinterpret_cast<uint4*>(
+                        const_cast<T*>(reinterpret_cast<const T*>(isv ? a.v : a.k)) + dst) + u;
+        *to = *from;
+    }
+}
 
 // ---------------------------------------------------------------------------
 // Balanced schedule.  Page-units are (sequence b, kv head) pairs in the order
@@ -188,6 +226,7 @@ __device__ inline int64_t build_segments(const DecodeArgs& a, const int* sP, con
         const int te = (pg + d.npages) * kPage;
         d.tok_end = te < sL[b] ? te : sL[b];
         d.direct = pg == 0 && seg_end == unit_end;
+        d.new_tok = seg_new_tok(a, b, pg, d.tok_end, sL[b]);
         const int64_t seg = wg + (int64_t)b * a.Hkv + kvh;
         d.po_off = seg * G * a.D;
         d.pl_off = seg * G;

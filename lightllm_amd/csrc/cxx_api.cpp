@@ -92,6 +92,32 @@ Tensor paged_attention(const Tensor& q, const int* block_table, int max_blocks_p
     return out;
 }
 
+Tensor paged_attention_append(const Tensor& q, const Tensor& k_new, const Tensor& v_new,
+                              const int* block_table, int max_blocks_per_seq, const int* seq_lens,
+                              BlockAllocator& allocator) {
+    const int T = q.size(0), Hq = q.size(1), D = q.size(2);
+    if (D > 256) throw std::runtime_error("paged_attention_append: head_dim too large");
+    require_pool_dtype(q.dtype(), allocator, "paged_attention_append");
+    require_pool_dtype(k_new.dtype(), allocator, "paged_attention_append");
+    require_pool_dtype(v_new.dtype(), allocator, "paged_attention_append");
+    require_device_pool(allocator, "paged_attention_append");
+    Tensor out({T, Hq, D}, q.dtype(), Device::CUDA);
+    if (T == 0) return out;
+    const int Hkv = allocator.num_kv_heads();
+    const int bs = allocator.block_size();
+    const int max_len = host_max(seq_lens, T);
+    const size_t ws = llkv_paged_decode_workspace_size(T, Hq, Hkv, D, bs, max_len, 0);
+    void* w = ws ? t_workspace.get(ws) : nullptr;
+    throw_if(llkv_paged_decode_append(out.raw(), q.raw(), k_new.raw(), v_new.raw(),
+                                      const_cast<void*>(allocator.k_storage_raw()),
+                                      const_cast<void*>(allocator.v_storage_raw()), block_table,
+                                      seq_lens, T, Hq, Hkv, D, bs, max_blocks_per_seq, max_len, 0,
+                                      1.0f / std::sqrt((float)D), static_cast<int>(q.dtype()), w, ws,
+                                      nullptr),
+             "paged_attention_append");
+    return out;
+}
+
 Tensor paged_prefill_varlen(const Tensor& q, const int* block_table, int max_blocks,
                             const int* cu_q, const int* seq_lens, int num_seqs, int max_q_len,
                             int max_seq_len, BlockAllocator& allocator, bool causal) {

@@ -230,11 +230,13 @@ void decode_split_kernel(DecodeArgs a) {
         d.cum = 0;
         d.tok_end = min((d.pg_begin + d.npages) * kPage, geo.L);
         d.direct = geo.nsplit == 1;
+        d.new_tok = seg_new_tok(a, b, d.pg_begin, d.tok_end, geo.L);
         const int64_t bh0 = (int64_t)b * a.Hq + hq0;
         d.po_off = (bh0 * a.S_max + split) * a.D;
         d.pl_off = bh0 * a.S_max + split;
     }
     __syncthreads();
+    store_new_row<T, Body::HD>(a, segs[0]);
     Body::round(a, sm, segs, 1, (int64_t)a.S_max * a.D, a.S_max);
 }
 
@@ -280,6 +282,7 @@ void decode_balanced_kernel(DecodeArgs a) {
         __syncthreads();
         const int n = s_n;
         p = s_next;
+        for (int i = 0; i < n; ++i) store_new_row<T, D>(a, segs[i]);
         Body::round(a, sm, segs, n, D, 1);   // ends with a barrier
     }
 }
@@ -505,14 +508,35 @@ extern "C" size_t llkv_paged_decode_workspace_size(int num_seqs, int num_q_heads
     return need;
 }
 
-extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
-                                 const void* v_pool, const int* block_table,
-                                 const int* seq_lens, int num_seqs, int num_q_heads,
-                                 int num_kv_heads, int head_dim, int block_size,
-                                 int max_blocks_per_seq, int max_seq_len, int num_splits,
-                                 float scale, int dtype, void* workspace,
-                                 size_t workspace_bytes, void* stream) {
-    const char* fn = "llkv_paged_decode";
+namespace llkv {
+namespace {
+
+// Fused append on the generic path: the new K/V row of (sequence, kv head) =
+// (blockIdx.y, blockIdx.x) goes to position len - 1 before the decode kernel
+// runs (any head_dim and page size).
+template <typename T>
+__global__ __launch_bounds__(64) void append_new_rows_kernel(DecodeArgs a) {
+    const int kvh = blockIdx.x, b = blockIdx.y;
+    const int L = clamp_len(a, b);
+    if (L <= 0) return;
+    const int phys = a.bt[(int64_t)b * a.max_blocks + (L - 1) / a.bs];
+    if (phys < 0) return;
+    const int64_t dst = (((int64_t)phys * a.bs + (L - 1) % a.bs) * a.Hkv + kvh) * a.D;
+    const int64_t src = ((int64_t)b * a.Hkv + kvh) * a.D;
+    T* kp = const_cast<T*>(reinterpret_cast<const T*>(a.k));
+    T* vp = const_cast<T*>(reinterpret_cast<const T*>(a.v));
+    for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
+        kp[dst + d] = reinterpret_cast<const T*>(a.knew)[src + d];
+        vp[dst + d] = reinterpret_cast<const T*>(a.vnew)[src + d];
+    }
+}
+
+int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_new,
+                      const void* v_new, const void* k_pool, const void* v_pool,
+                      const int* block_table, const int* seq_lens, int num_seqs, int num_q_heads,
+                      int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq,
+                      int max_seq_len, int num_splits, float scale, int dtype, void* workspace,
+                      size_t workspace_bytes, void* stream) {
     if (num_seqs == 0) return LLKV_OK;
     if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
         block_size <= 0 || max_blocks_per_seq <= 0 || num_splits < 0)
@@ -534,7 +558,7 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
     // The tuned bodies need 16-token pages, 16-byte aligned rows and pointers.
     const size_t es = dtype_bytes(dtype);
     const bool aligned = (((uintptr_t)q | (uintptr_t)out | (uintptr_t)k_pool |
-                           (uintptr_t)v_pool) & 15) == 0 &&
+                           (uintptr_t)v_pool | (uintptr_t)k_new | (uintptr_t)v_new) & 15) == 0 &&
                          ((size_t)num_kv_heads * head_dim * es) % 16 == 0;
     Kernels ks;
     if (block_size == kPage && aligned) {
@@ -566,6 +590,8 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
     a.scale_log2 = scale * kLog2e;
     a.nwg = 0;
     a.plan = nullptr;
+    a.knew = k_new;
+    a.vnew = v_new;
     char* ws = reinterpret_cast<char*>(workspace);
     hipStream_t st = (hipStream_t)stream;
 
@@ -599,6 +625,13 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
             dim3 grid(p.S_max, num_kv_heads, num_seqs);
             ks.split<<<grid, 64 * kDecodeWaves, 0, st>>>(a);
         } else {
+            if (k_new != nullptr) {   // append first, then the plain generic decode
+                dim3 agrid(num_kv_heads, num_seqs);
+                if (dtype == LLKV_DTYPE_F32) append_new_rows_kernel<float><<<agrid, 64, 0, st>>>(a);
+                else if (dtype == LLKV_DTYPE_F16) append_new_rows_kernel<_Float16><<<agrid, 64, 0, st>>>(a);
+                else append_new_rows_kernel<bf16_t><<<agrid, 64, 0, st>>>(a);
+                a.knew = a.vnew = nullptr;
+            }
             dim3 grid(p.S_max, num_q_heads, num_seqs);
             if (dtype == LLKV_DTYPE_F32) decode_generic_kernel<float><<<grid, 64, 0, st>>>(a);
             else if (dtype == LLKV_DTYPE_F16) decode_generic_kernel<_Float16><<<grid, 64, 0, st>>>(a);
@@ -612,4 +645,36 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
     else if (dtype == LLKV_DTYPE_F16) launch_merge<_Float16>(balanced, head_dim, grid, st, a);
     else launch_merge<bf16_t>(balanced, head_dim, grid, st, a);
     return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace llkv
+
+extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
+                                 const void* v_pool, const int* block_table,
+                                 const int* seq_lens, int num_seqs, int num_q_heads,
+                                 int num_kv_heads, int head_dim, int block_size,
+                                 int max_blocks_per_seq, int max_seq_len, int num_splits,
+                                 float scale, int dtype, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    return paged_decode_impl("llkv_paged_decode", out, q, nullptr, nullptr, k_pool, v_pool,
+                             block_table, seq_lens, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                             block_size, max_blocks_per_seq, max_seq_len, num_splits, scale, dtype,
+                             workspace, workspace_bytes, stream);
+}
+
+extern "C" int llkv_paged_decode_append(void* out, const void* q, const void* k_new,
+                                        const void* v_new, void* k_pool, void* v_pool,
+                                        const int* block_table, const int* seq_lens, int num_seqs,
+                                        int num_q_heads, int num_kv_heads, int head_dim,
+                                        int block_size, int max_blocks_per_seq, int max_seq_len,
+                                        int num_splits, float scale, int dtype, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    const char* fn = "llkv_paged_decode_append";
+    if (num_seqs > 0 && (!k_new || !v_new))
+        return set_error(LLKV_ERR_INVALID, "%s: null pointer", fn);
+    return paged_decode_impl(fn, out, q, k_new, v_new, k_pool, v_pool, block_table, seq_lens,
+                             num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                             max_blocks_per_seq, max_seq_len, num_splits, scale, dtype, workspace,
+                             workspace_bytes, stream);
 }

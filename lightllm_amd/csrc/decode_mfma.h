@@ -194,6 +194,8 @@ struct MfmaDecode {
 
         // State of the current segment.
         int cur = -1, sb = 0, skvh = 0, spg = 0, scum = 0, stok = 0;
+        // Fused append: page and row of the segment's new token (-1: none).
+        int snew_pg = -1, snew_r = 0;
         int next_cum = 0;   // first page of the next segment (register copy)
         typename Ops::QReg qop[Ops::NQ];
         mf32x4 o[DT];
@@ -238,6 +240,9 @@ struct MfmaDecode {
                 spg = segs[s].pg_begin;
                 scum = segs[s].cum;
                 stok = segs[s].tok_end;
+                const int nt = __builtin_amdgcn_readfirstlane(segs[s].new_tok);
+                snew_pg = nt >= 0 ? nt / kPage : -1;
+                snew_r = nt % kPage;
                 // Q^T operand: column c is query head kvh*G + c (zero beyond G).
                 const T* qrow = reinterpret_cast<const T*>(a.q) + ((int64_t)sb * a.Hq + skvh * G + c) * D;
                 Ops::load_q(qrow, c < G, g, a.scale_log2, qop);
@@ -250,12 +255,18 @@ struct MfmaDecode {
             const int64_t phys = max(__builtin_amdgcn_readlane(tbl, k - tbl_k0), 0);
 
             // K row of the lane's token c; V rows 4g + i, dims 64h + 4c .. + 3.
+            // The new token of a fused append is read from the caller's buffers
+            // (its pool row is being written by this work-group).
+            const bool newpage = pg == snew_pg;   // uniform
+            const int64_t nrow = ((int64_t)sb * a.Hkv + skvh) * D;   // the new rows' offset
             const T* kp = reinterpret_cast<const T*>(a.k) + (int64_t)skvh * D + (phys * kPage + c) * row_elems;
+            if (newpage && c == snew_r) kp = reinterpret_cast<const T*>(a.knew) + nrow;
             Ops::load_k(kp, g, kr);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const T* vp = reinterpret_cast<const T*>(a.v) + (int64_t)skvh * D +
                               (phys * kPage + 4 * g + i) * row_elems + 4 * c;
+                if (newpage && 4 * g + i == snew_r) vp = reinterpret_cast<const T*>(a.vnew) + nrow + 4 * c;
 #pragma unroll
                 for (int h = 0; h < VH; ++h) vr[h][i] = Ops::load_v4(vp + 64 * h);
             }

@@ -64,4 +64,4 @@ extern "C" const char* llkv_status_string(int status) {
     return "unknown status";
 }
 
-extern "C" int llkv_abi_version(void) { return 3; }
+extern "C" int llkv_abi_version(void) { return 4; }

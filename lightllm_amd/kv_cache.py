@@ -281,6 +281,36 @@ def paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     return out
 
 
+def paged_decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                        k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Tensor,
+                        seq_lens: torch.Tensor, max_seq_len: int, num_splits: int = 0,
+                        scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                        workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Fused KV append + paged decode: the new rows k_new / v_new [B, Hkv, D] go to position
+    seq_lens[b] - 1 of each sequence (seq_lens count the new token), then decode attention over
+    [0, seq_lens[b]); equal to append_kv followed by paged_decode."""
+    _require(q, k_pool.dtype, "q")
+    _require(k_new, k_pool.dtype, "k_new")
+    _require(v_new, k_pool.dtype, "v_new")
+    _require(block_table, torch.int32, "block_table")
+    _require(seq_lens, torch.int32, "seq_lens")
+    b, hq, d = q.shape
+    nb, bs, hkv, _ = k_pool.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        out = torch.empty_like(q)
+    ws = decode_workspace_bytes(b, hq, hkv, d, bs, max_seq_len, num_splits)
+    if ws and (workspace is None or workspace.numel() * workspace.element_size() < ws):
+        workspace = _workspace(ws, q.device)
+    check(lib().llkv_paged_decode_append(_ptr(out), _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_pool),
+                                         _ptr(v_pool), _ptr(block_table), _ptr(seq_lens), b, hq, hkv,
+                                         d, bs, block_table.shape[1], max_seq_len, num_splits, scale,
+                                         dtype_code(q.dtype), _ptr(workspace) if ws else None, ws,
+                                         _stream(stream)))
+    return out
+
+
 def paged_attention(q: torch.Tensor, block_table: torch.Tensor, max_blocks_per_seq: int,
                     seq_lens: torch.Tensor, allocator: BlockAllocator,
                     max_seq_len: Optional[int] = None) -> torch.Tensor:

@@ -40,7 +40,7 @@ def test_python_bindings_cover_the_header():
 
 def test_version_and_status_strings():
     lib = L.lib()
-    assert lib.llkv_abi_version() == 3
+    assert lib.llkv_abi_version() == 4
     assert L.status_string(0) == "ok"
     assert "invalid" in L.status_string(1)
     assert "unsupported" in L.status_string(2) or "support" in L.status_string(2)

@@ -210,6 +210,52 @@ def test_rope_append_step_with_device_slots_then_decode():
     check_lowp(out, ref, "decode after rope_append", 2e-3)
 
 
+FUSED = [
+    # (name, B, Hq, Hkv, D, dtype, num_splits, length range)
+    ("f32_cfg2_auto", 64, 14, 2, 64, torch.float32, 0, (127, 2048)),
+    ("f16_llama_balanced", 300, 32, 8, 128, torch.float16, 0, (1, 1500)),
+    ("bf16_S4", 40, 14, 2, 64, torch.bfloat16, 4, (1, 700)),
+    ("f16_G16_S16", 8, 16, 1, 64, torch.float16, 16, (500, 5000)),
+    ("f32_generic_D67", 12, 4, 2, 67, torch.float32, 0, (1, 300)),
+]
+
+
+@pytest.mark.parametrize("name,B,hq,hkv,d,dtype,S,lr", FUSED, ids=[c[0] for c in FUSED])
+def test_decode_append_equals_append_then_decode(name, B, hq, hkv, d, dtype, S, lr):
+    """llkv_paged_decode_append gives the same bits as llkv_append followed by llkv_paged_decode:
+    output and both pools."""
+    say(f"fused append + decode {name}")
+    g = torch.Generator().manual_seed(len(name) + 3)
+    lens = torch.randint(lr[0], lr[1] + 1, (B,), generator=g, dtype=torch.int32)
+    lens[0] = 1            # only the new token
+    lens[1 % B] = 16       # new token ends a page
+    lens[2 % B] = 17       # new token opens a page
+    mb = (int(lens.max()) + 15) // 16
+    nb = int(sum((int(L) + 15) // 16 for L in lens)) + 8
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    table, _ = wl._tables([int(L) for L in lens], perm, mb)
+    if B > 3:   # a sequence whose new token's page is missing from the table: no pool write
+        table[3, (int(lens[3]) - 1) // 16] = -1
+    kp = torch.randn(nb, 16, hkv, d, generator=g).to(dtype).to(DEV)
+    vp = torch.randn(nb, 16, hkv, d, generator=g).to(dtype).to(DEV)
+    q = torch.randn(B, hq, d, generator=g).to(dtype).to(DEV)
+    kn = torch.randn(B, hkv, d, generator=g).to(dtype).to(DEV)
+    vn = torch.randn(B, hkv, d, generator=g).to(dtype).to(DEV)
+    td, ld = table.to(DEV), lens.to(DEV)
+    kp2, vp2 = kp.clone(), vp.clone()
+    fused = kc.paged_decode_append(q, kn, vn, kp, vp, td, ld, int(lens.max()), num_splits=S)
+    slots = []
+    for b in range(B):
+        pos = int(lens[b]) - 1
+        phys = int(table[b, pos // 16])
+        slots.append(phys * 16 + pos % 16 if phys >= 0 else -1)
+    kc.append_kv(kn, vn, torch.tensor(slots, dtype=torch.int64, device=DEV), kp2, vp2)
+    ref = kc.paged_decode(q, kp2, vp2, td, ld, int(lens.max()), num_splits=S)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(kp), bits(kp2)) and np.array_equal(bits(vp), bits(vp2)), "pools"
+    assert np.array_equal(bits(fused), bits(ref)), "output"
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_scatter_and_gather_round_trip(dtype):
     say(f"scatter/gather dtype={dtype}")
