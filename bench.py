@@ -125,8 +125,14 @@ def bench_decode(args, torch, kc, wl):
         torch.cuda.synchronize()
         return t0.elapsed_time(t1) * 1e3 / k
 
+    def step_fused(i):   # the same append + decode as one llkv_paged_decode_append call
+        layer = i % L
+        kc.paged_decode_append(qs[layer], kn[layer], vn[layer], kps[layer], vps[layer], table, lens,
+                               max_len, out=outs[layer], workspace=ws)
+
     step_us = replay_us(step, args.steps)
     dec_us = replay_us(decode_only, args.steps)
+    fused_us = replay_us(step_fused, args.steps)
 
     # Eager loop with HIP events around each decode call (host-launch gaps included).
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -152,7 +158,7 @@ def bench_decode(args, torch, kc, wl):
     dec_bytes_pages = wl.decode_bytes(case, exact_tokens=False)
     app_bytes = wl.append_bytes(case)
     return {
-        "case": case, "host_pools": (ke, ve), "step_ms": step_us / 1e3,
+        "case": case, "host_pools": (ke, ve), "step_ms": step_us / 1e3, "step_fused_us": fused_us,
         "decode_us_mean": dec_us, "decode_us_eager_median": statistics.median(eager_us),
         "decode_bytes": dec_bytes, "decode_bytes_pages": dec_bytes_pages, "append_bytes": app_bytes,
         "parity_ok": ok, "max_abs_err": float(err.max()),
@@ -506,6 +512,7 @@ def main():
                    "batch": 64, "layers_rotated": args.layers},
         "us_per_layer": round(step_us, 2),
         "step_GBps_incl_append": round(step_gbs, 1),
+        "us_per_layer_fused_append": round(dec["step_fused_us"], 2),
         "decode_us": round(dec["decode_us_mean"], 2),
         "decode_us_eager_median": round(dec["decode_us_eager_median"], 2),
         "decode_GBps_page_granular": round(dec["decode_bytes_pages"] / (dec["decode_us_mean"] * 1e-6) / 1e9, 1),

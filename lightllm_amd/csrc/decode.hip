@@ -332,44 +332,54 @@ Kernels kernels_of() {
     return k;
 }
 
-template <typename T, int D>
+template <typename T, int D, bool A>
 Kernels pick_mfma16_g(int G) {
     switch (G) {
-        case 1: return kernels_of<MfmaDecode<T, D, 1>>();
-        case 2: return kernels_of<MfmaDecode<T, D, 2>>();
-        case 4: return kernels_of<MfmaDecode<T, D, 4>>();
-        case 7: return kernels_of<MfmaDecode<T, D, 7>>();
-        case 8: return kernels_of<MfmaDecode<T, D, 8>>();
-        case 16: return kernels_of<MfmaDecode<T, D, 16>>();
+        case 1: return kernels_of<MfmaDecode<T, D, 1, A>>();
+        case 2: return kernels_of<MfmaDecode<T, D, 2, A>>();
+        case 4: return kernels_of<MfmaDecode<T, D, 4, A>>();
+        case 7: return kernels_of<MfmaDecode<T, D, 7, A>>();
+        case 8: return kernels_of<MfmaDecode<T, D, 8, A>>();
+        case 16: return kernels_of<MfmaDecode<T, D, 16, A>>();
     }
     return Kernels();
 }
 
 // fp16 / bf16 pools: the MFMA body (decode_mfma.h).
-template <typename T>
+template <typename T, bool A>
 Kernels pick_mfma16(int D, int G) {
-    if (D == 64) return pick_mfma16_g<T, 64>(G);
-    if (D == 128) return pick_mfma16_g<T, 128>(G);
+    if (D == 64) return pick_mfma16_g<T, 64, A>(G);
+    if (D == 128) return pick_mfma16_g<T, 128, A>(G);
     return Kernels();
 }
 
-template <int D>
+template <int D, bool A>
 Kernels pick_mfma_f32_g(int G) {
     switch (G) {
-        case 1: return kernels_of<MfmaDecode<float, D, 1>>();
-        case 2: return kernels_of<MfmaDecode<float, D, 2>>();
-        case 4: return kernels_of<MfmaDecode<float, D, 4>>();
-        case 7: return kernels_of<MfmaDecode<float, D, 7>>();
-        case 8: return kernels_of<MfmaDecode<float, D, 8>>();
-        case 16: return kernels_of<MfmaDecode<float, D, 16>>();
+        case 1: return kernels_of<MfmaDecode<float, D, 1, A>>();
+        case 2: return kernels_of<MfmaDecode<float, D, 2, A>>();
+        case 4: return kernels_of<MfmaDecode<float, D, 4, A>>();
+        case 7: return kernels_of<MfmaDecode<float, D, 7, A>>();
+        case 8: return kernels_of<MfmaDecode<float, D, 8, A>>();
+        case 16: return kernels_of<MfmaDecode<float, D, 16, A>>();
     }
     return Kernels();
 }
 
 // fp32 pools: the MFMA body (decode_mfma.h).
+template <bool A>
 Kernels pick_f32(int D, int G) {
-    if (D == 64) return pick_mfma_f32_g<64>(G);
-    if (D == 128) return pick_mfma_f32_g<128>(G);
+    if (D == 64) return pick_mfma_f32_g<64, A>(G);
+    if (D == 128) return pick_mfma_f32_g<128, A>(G);
+    return Kernels();
+}
+
+// The tuned kernels of a pool type, plain or fused-append.
+template <bool A>
+Kernels pick_tuned(int dtype, int D, int G) {
+    if (dtype == LLKV_DTYPE_F32) return pick_f32<A>(D, G);
+    if (dtype == LLKV_DTYPE_F16) return pick_mfma16<_Float16, A>(D, G);
+    if (dtype == LLKV_DTYPE_BF16) return pick_mfma16<bf16_t, A>(D, G);
     return Kernels();
 }
 
@@ -562,9 +572,7 @@ int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_ne
                          ((size_t)num_kv_heads * head_dim * es) % 16 == 0;
     Kernels ks;
     if (block_size == kPage && aligned) {
-        if (dtype == LLKV_DTYPE_F32) ks = pick_f32(head_dim, G);
-        else if (dtype == LLKV_DTYPE_F16) ks = pick_mfma16<_Float16>(head_dim, G);
-        else if (dtype == LLKV_DTYPE_BF16) ks = pick_mfma16<bf16_t>(head_dim, G);
+        ks = k_new ? pick_tuned<true>(dtype, head_dim, G) : pick_tuned<false>(dtype, head_dim, G);
     }
     const int max_pages_hint = (max_seq_len + block_size - 1) / block_size;
     bool balanced = false;

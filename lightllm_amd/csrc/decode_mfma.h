@@ -138,7 +138,10 @@ __device__ inline mf32x4 ScoreOps16<bf16_t, 128>::mma(const mu32x4& a, const mu3
 template <int D> struct ScoreOps<_Float16, D> : ScoreOps16<_Float16, D> {};
 template <int D> struct ScoreOps<bf16_t, D> : ScoreOps16<bf16_t, D> {};
 
-template <typename TT, int D, int G>
+// A = true: the fused-append variant (llkv_paged_decode_append), which reads
+// the segment's new token from the caller's buffers; the plain variant's page
+// loop has no trace of it.
+template <typename TT, int D, int G, bool A = false>
 struct MfmaDecode {
     static_assert(G >= 1 && G <= 16, "up to 16 query heads per KV head");
     static_assert(D % 64 == 0, "head_dim multiple of 64");
@@ -240,9 +243,11 @@ struct MfmaDecode {
                 spg = segs[s].pg_begin;
                 scum = segs[s].cum;
                 stok = segs[s].tok_end;
-                const int nt = __builtin_amdgcn_readfirstlane(segs[s].new_tok);
-                snew_pg = nt >= 0 ? nt / kPage : -1;
-                snew_r = nt % kPage;
+                if constexpr (A) {
+                    const int nt = __builtin_amdgcn_readfirstlane(segs[s].new_tok);
+                    snew_pg = nt >= 0 ? nt / kPage : -1;
+                    snew_r = nt % kPage;
+                }
                 // Q^T operand: column c is query head kvh*G + c (zero beyond G).
                 const T* qrow = reinterpret_cast<const T*>(a.q) + ((int64_t)sb * a.Hq + skvh * G + c) * D;
                 Ops::load_q(qrow, c < G, g, a.scale_log2, qop);
@@ -257,7 +262,7 @@ struct MfmaDecode {
             // K row of the lane's token c; V rows 4g + i, dims 64h + 4c .. + 3.
             // The new token of a fused append is read from the caller's buffers
             // (its pool row is being written by this work-group).
-            const bool newpage = pg == snew_pg;   // uniform
+            const bool newpage = A && pg == snew_pg;   // uniform
             const int64_t nrow = ((int64_t)sb * a.Hkv + skvh) * D;   // the new rows' offset
             const T* kp = reinterpret_cast<const T*>(a.k) + (int64_t)skvh * D + (phys * kPage + c) * row_elems;
             if (newpage && c == snew_r) kp = reinterpret_cast<const T*>(a.knew) + nrow;
@@ -270,6 +275,9 @@ struct MfmaDecode {
 #pragma unroll
                 for (int h = 0; h < VH; ++h) vr[h][i] = Ops::load_v4(vp + 64 * h);
             }
+            // The fused variant's pointer selects make the scheduler sink the V
+            // loads next to their MFMAs; keep all of the page's loads first.
+            if constexpr (A) __builtin_amdgcn_sched_barrier(0);
 
             const mf32x4 sacc = Ops::scores(kr, qop, a.scale_log2);
             const int t0 = pg * kPage + 4 * g;
