@@ -337,12 +337,63 @@ static void test_rope_append_gpu() {
     (void)hipFree(slots);
 }
 
+// paged_attention_append == append_kv_slots then paged_attention, bit for bit.
+static void test_decode_append_gpu() {
+    const int Hq = 14, Hkv = 2, D = 64, bs = 16, nb = 64, B = 3, mb = 4;
+    BlockAllocator fa(nb, bs, Hkv, D), ua(nb, bs, Hkv, D);
+    const size_t pool = (size_t)nb * bs * Hkv * D;
+    std::vector<float> kp = rnd(pool, 41), vp = rnd(pool, 42);
+    for (BlockAllocator* a : {&fa, &ua}) {
+        (void)hipMemcpy(const_cast<void*>(a->k_storage_raw()), kp.data(), pool * 4, hipMemcpyHostToDevice);
+        (void)hipMemcpy(const_cast<void*>(a->v_storage_raw()), vp.data(), pool * 4, hipMemcpyHostToDevice);
+    }
+    const int lens[B] = {5, 16, 40};   // after the append: new tokens at 4, 15, 39
+    std::vector<int> table((size_t)B * mb, -1);
+    int next = 3;
+    for (int b = 0; b < B; ++b)
+        for (int p = 0; p < (lens[b] + bs - 1) / bs; ++p) table[(size_t)b * mb + p] = next++ * 2 % nb;
+    std::vector<int64_t> slots(B);
+    for (int b = 0; b < B; ++b) {
+        const int pos = lens[b] - 1;
+        slots[b] = (int64_t)table[(size_t)b * mb + pos / bs] * bs + pos % bs;
+    }
+    Tensor d_bt({B * mb}, DType::I32, Device::CUDA), d_sl({B}, DType::I32, Device::CUDA);
+    d_bt.copy_from(table.data(), table.size() * 4);
+    d_sl.copy_from(lens, sizeof(lens));
+    std::vector<float> q = rnd((size_t)B * Hq * D, 43), kn = rnd((size_t)B * Hkv * D, 44),
+                       vn = rnd((size_t)B * Hkv * D, 45);
+    Tensor tq({B, Hq, D}, DType::F32, Device::CUDA), tk({B, Hkv, D}, DType::F32, Device::CUDA),
+        tv({B, Hkv, D}, DType::F32, Device::CUDA);
+    tq.copy_from(q.data(), q.size() * 4);
+    tk.copy_from(kn.data(), kn.size() * 4);
+    tv.copy_from(vn.data(), vn.size() * 4);
+    int64_t* d_slots = nullptr;
+    (void)hipMalloc(&d_slots, B * sizeof(int64_t));
+    (void)hipMemcpy(d_slots, slots.data(), B * sizeof(int64_t), hipMemcpyHostToDevice);
+    Tensor fused = paged_attention_append(tq, tk, tv, d_bt.data<int>(), mb, d_sl.data<int>(), fa);
+    append_kv_slots(tk, tv, d_slots, ua);
+    Tensor plain = paged_attention(tq, d_bt.data<int>(), mb, d_sl.data<int>(), ua);
+    (void)hipDeviceSynchronize();
+    std::vector<float> of((size_t)B * Hq * D), op(of.size()), fk(pool), uk(pool), fv(pool), uv(pool);
+    fused.copy_to(of.data(), of.size() * 4);
+    plain.copy_to(op.data(), op.size() * 4);
+    (void)hipMemcpy(fk.data(), fa.k_storage_raw(), pool * 4, hipMemcpyDeviceToHost);
+    (void)hipMemcpy(uk.data(), ua.k_storage_raw(), pool * 4, hipMemcpyDeviceToHost);
+    (void)hipMemcpy(fv.data(), fa.v_storage_raw(), pool * 4, hipMemcpyDeviceToHost);
+    (void)hipMemcpy(uv.data(), ua.v_storage_raw(), pool * 4, hipMemcpyDeviceToHost);
+    CHECK("decode_append_output_bit_exact", std::memcmp(of.data(), op.data(), of.size() * 4) == 0);
+    CHECK("decode_append_pools_bit_exact", std::memcmp(fk.data(), uk.data(), pool * 4) == 0 &&
+                                               std::memcmp(fv.data(), uv.data(), pool * 4) == 0);
+    (void)hipFree(d_slots);
+}
+
 int main(int argc, char** argv) {
     const bool gpu = argc > 1 && std::strcmp(argv[1], "gpu") == 0;
     if (gpu) {
         std::printf("== C++ API on the GPU\n");
         test_ops_gpu();
         test_rope_append_gpu();
+        test_decode_append_gpu();
     } else {
         std::printf("== BlockAllocator / BlockTable (CPU)\n");
         test_allocator_cpu();
