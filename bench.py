@@ -430,7 +430,9 @@ def rocprof_traffic(fetch_dir, write_dir, cal_fetch_dir, cal_write_dir) -> None:
     print(f"scale: fetch {f_scale:.3f} B per unit, write {w_scale:.3f} B per unit")
     total = 0.0
     for k in sorted(set(fetch) | set(write)):
-        if "decode" not in k:
+        # configuration 2's plain decode: the fp32 split and merge kernels (not the
+        # fused-append instantiation the run also times)
+        if "decode" not in k or "float" not in k or "true" in k:
             continue
         fb = fetch.get(k, 0.0) * f_scale
         wb = write.get(k, 0.0) * w_scale
