@@ -198,21 +198,24 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)kvh * D;
     const T* vg = reinterpret_cast<const T*>(a.v) + (int64_t)kvh * D;
 
-    // ---- Q^T operands (B of S^T = K Q^T), kept in registers -------------
+    // ---- Q^T operands (B of S^T = K Q^T), kept in registers; loaded after the
+    // page ids so that their latency overlaps the first tile's ------------
     uint4 qop[2][KS];
     const T* qg = reinterpret_cast<const T*>(a.q);
+    auto load_q = [&]() {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int ql = q_lo + w * WQ + nt * 16 + c16;
+        for (int nt = 0; nt < 2; ++nt) {
+            const int ql = q_lo + w * WQ + nt * 16 + c16;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            if (ql < P)
-                qop[nt][ks] = *reinterpret_cast<const uint4*>(
-                    qg + ((int64_t)(q0 + ql) * a.Hq + hq) * D + ks * 32 + g * 8);
-            else
-                qop[nt][ks] = make_uint4(0, 0, 0, 0);
+            for (int ks = 0; ks < KS; ++ks) {
+                if (ql < P)
+                    qop[nt][ks] = *reinterpret_cast<const uint4*>(
+                        qg + ((int64_t)(q0 + ql) * a.Hq + hq) * D + ks * 32 + g * 8);
+                else
+                    qop[nt][ks] = make_uint4(0, 0, 0, 0);
+            }
         }
-    }
+    };
 
     // Absolute position of this lane's two query columns; rows >= P see nothing.
     int qpos[2];
@@ -308,10 +311,11 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     auto stage_pages = [&](int base) {
         tbase = base;
         for (int i = tid; i < kPageWindow; i += 256) sm.pages[i] = bt[min(base + i, last_page)];
-        __syncthreads();
+        lds_barrier();   // the page ids are in LDS; no global load needs to have landed
     };
     if (t_begin < t_end) {
         stage_pages(4 * t_begin);
+        load_q();
         load_tile(t_begin, kr, vr);
         store_tile(0, kr, vr);
     }
