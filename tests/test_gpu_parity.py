@@ -655,6 +655,55 @@ def _compact_pages(kp: torch.Tensor, vp: torch.Tensor, table: torch.Tensor):
     return np_pool(kp.index_select(0, idx)), np_pool(vp.index_select(0, idx)), t
 
 
+def test_pool_beyond_2pow32_elements():
+    """Pools of 9.8e9 fp16 elements (19.7 GB each): append, decode and prefill over pages at
+    the top of the pool, where element offsets pass 2^33, against the oracle on those pages."""
+    say("pools beyond 2^32 elements (600000 pages x 16 x 8 x 128 fp16 each)")
+    nb, hkv, hq, d = 600000, 8, 32, 128
+    kp = torch.empty(nb, 16, hkv, d, dtype=torch.float16, device=DEV)
+    vp = torch.empty_like(kp)
+    g = torch.Generator().manual_seed(91)
+    lens = [100, 37, 250]
+    pages = [(L + 15) // 16 for L in lens]
+    ids = torch.tensor([nb - 1 - 3 * i for i in range(sum(pages))], dtype=torch.int32)
+    table, _ = wl._tables(lens, ids, max(pages))
+    used = ids.long().to(DEV)
+    kp.index_copy_(0, used, torch.randn(used.numel(), 16, hkv, d, generator=g).to(torch.float16).to(DEV))
+    vp.index_copy_(0, used, torch.randn(used.numel(), 16, hkv, d, generator=g).to(torch.float16).to(DEV))
+    td, ld = table.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV)
+    # append the last token of each sequence through the slot mapping, then decode
+    kn = torch.randn(3, hkv, d, generator=g).to(torch.float16).to(DEV)
+    vn = torch.randn(3, hkv, d, generator=g).to(torch.float16).to(DEV)
+    slots = kc.build_slots(td, torch.arange(4, dtype=torch.int32, device=DEV), ld - 1, 3)
+    kc.append_kv(kn, vn, slots, kp, vp)
+    q = torch.randn(3, hq, d, generator=g).to(torch.float16).to(DEV)
+    out = kc.paged_decode(q, kp, vp, td, ld, max(lens))
+    # prefill: the last 20 tokens of each sequence over the rest
+    P = 20
+    qp = torch.randn(3 * P, hq, d, generator=g).to(torch.float16).to(DEV)
+    cu = torch.arange(0, 3 * P + 1, P, dtype=torch.int32, device=DEV)
+    outp = kc.paged_prefill(qp, kp, vp, td, cu, ld, P, max(lens), causal=True)
+    torch.cuda.synchronize()
+    kh, vh, th = _compact_pages(kp, vp, table)
+    sl = slots.cpu().numpy()
+    for b in range(3):
+        pos = lens[b] - 1
+        assert sl[b] == int(table[b, pos // 16]) * 16 + pos % 16
+    kr = kh.reshape(-1, hkv, d)
+    for b in range(3):   # the appended rows landed in the compacted copy's renumbered pages
+        pos = lens[b] - 1
+        row = int(th[b, pos // 16]) * 16 + pos % 16
+        assert np.array_equal(kr[row], kn[b].float().cpu().numpy())
+    ref = oracle.paged_decode(q.float().cpu().numpy(), kh, vh, th.numpy(), np.array(lens), f64=True,
+                              nthreads=16)
+    check_lowp(out, ref, "decode, pool beyond 2^32 elements", 2e-3)
+    refp = oracle.paged_prefill(qp.float().cpu().numpy(), cu.cpu().numpy(), kh, vh, th.numpy(),
+                                np.array(lens, dtype=np.int32), True, f64=True, nthreads=16)
+    check_lowp(outp, refp, "prefill, pool beyond 2^32 elements", 2e-3)
+    del kp, vp
+    torch.cuda.empty_cache()
+
+
 def test_config5_mixed_step():
     """Configuration 5 at full size, one step: append (256 decode tokens + 4 x 1024 chunk
     tokens), decode of 256 lognormal contexts, then causal prefill of the chunks over a shared
