@@ -39,6 +39,13 @@ public:
                    PrefixCachePolicy policy = PrefixCachePolicy::Hash,
                    DType kv_dtype = DType::F32, PoolStorage storage = PoolStorage::Device);
 
+    /// Pages of (K + V) pools that fit in budget_bytes for this element type (new; the
+    /// reference's engine sizes pools as fp32 in EngineServer's constructor,
+    /// src/engine/engine_server.cpp:418-422 and :470-476).  At 288 GB and 16-token pages of
+    /// 8 kv heads x 128 dims in fp16 that is 4.4 million pages; clamped to INT32_MAX.
+    static int blocks_for_budget(size_t budget_bytes, int block_size, int num_kv_heads, int head_dim,
+                                 DType kv_dtype);
+
     int allocate(uint64_t token_hash = 0);
     int allocate_tokens(const int* tokens, int n_tokens, int start_pos,
                         std::vector<int>& out_blocks);

@@ -15,6 +15,8 @@
 //  reset:           all metadata, a fresh cache, zeroed pools.
 #include "lightllm/kv_cache/block_allocator.h"
 
+#include <cstdint>
+
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -162,6 +164,15 @@ void BlockAllocator::increment_ref(int block_id) {
     if (block_id < 0 || block_id >= num_blocks_) return;
     ++blocks_[block_id].ref_count;
     prefix_cache_->increment_ref(block_id);
+}
+
+int BlockAllocator::blocks_for_budget(size_t budget_bytes, int block_size, int num_kv_heads,
+                                      int head_dim, DType kv_dtype) {
+    const size_t esize = kv_dtype == DType::F32 ? 4 : 2;
+    const size_t per_block = (size_t)block_size * num_kv_heads * head_dim * esize * 2;
+    if (per_block == 0) return 0;
+    const size_t n = budget_bytes / per_block;
+    return n > (size_t)INT32_MAX ? INT32_MAX : (int)n;
 }
 
 void BlockAllocator::zero_pools() {

@@ -44,6 +44,11 @@ static void test_allocator_cpu() {
     CHECK("block_size", alloc.block_size() == 16);
     CHECK("hkv", alloc.num_kv_heads() == 2);
     CHECK("hdim", alloc.head_dim() == 64);
+    // 288 GB of fp16 K+V, Llama-3-8B heads: 288e9 / (16 * 8 * 128 * 2 B * 2) pages
+    CHECK("budget_288GB_fp16", BlockAllocator::blocks_for_budget(288000000000ull, 16, 8, 128, DType::F16) ==
+                                   (int)(288000000000ull / 65536));
+    CHECK("budget_fp32_half", BlockAllocator::blocks_for_budget(1ull << 30, 16, 2, 64, DType::F32) ==
+                                  2 * BlockAllocator::blocks_for_budget(1ull << 30, 16, 2, 128, DType::F32));
     int b0 = alloc.allocate(0x123), b1 = alloc.allocate(0x456);
     CHECK("fifo_0", b0 == 0);
     CHECK("fifo_1", b1 == 1);
