@@ -15,10 +15,9 @@
 //  reset:           all metadata, a fresh cache, zeroed pools.
 #include "lightllm/kv_cache/block_allocator.h"
 
-#include <cstdint>
-
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstring>
 #include <stdexcept>
 
