@@ -521,7 +521,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "llkv_paged_decode (automatic schedule for this batch: "
-                               "decode_split_kernel<MfmaDecode<float,64,7>> S=8, then "
+                               "decode_split_kernel<MfmaDecode<float,64,7>> S=10, then "
                                "decode_merge_kernel<float,1>)",
                      "bytes_per_launch": dec["decode_bytes"],
                      "timing": "HIP events on the launch stream around a HIP-graph replay of "

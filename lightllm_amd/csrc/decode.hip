@@ -456,10 +456,11 @@ int balanced_wgs(DecodeFn fn, int64_t page_units_bound) {
 
 // Automatic schedule.  With few (sequence, kv head) units against the
 // resident work-group count, fixed splits of each unit fill the GPU in one
-// pass (S ~ 0.8 x resident / units; 1 KB-page reads per wave stay long enough
-// to keep the loads streaming); with many units (a large batch of uneven
-// lengths) the balanced schedule shares the pages equally instead.
+// pass (S ~ resident / units, or 0.8 x that when the longest sequence gives
+// each wave more than kShortChainPages pages); with many units (a large batch
+// of uneven lengths) the balanced schedule shares the pages equally instead.
 constexpr int kAutoMaxSplits = 64;
+constexpr int kShortChainPages = 4;   // pages per wave up to which a split is latency-bound
 
 struct AutoChoice {
     bool balanced;
@@ -474,7 +475,11 @@ AutoChoice auto_schedule(const Kernels& ks, int B, int Hkv, int max_pages) {
         c.balanced = true;
         return c;
     }
-    int64_t S = (cap * 4 / 5 + units - 1) / units;
+    // One resident set of work-groups when each wave's chain of pages stays short
+    // (latency-bound: every extra work-group adds loads in flight); 0.8 of it when
+    // the chains are long (bandwidth-bound: extra work-groups only contend).
+    int64_t S = (cap + units - 1) / units;
+    if ((int64_t)max_pages > S * kDecodeWaves * kShortChainPages) S = (cap * 4 / 5 + units - 1) / units;
     S = std::max<int64_t>(1, std::min<int64_t>({S, (int64_t)kAutoMaxSplits, (int64_t)std::max(1, max_pages)}));
     c.splits = (int)S;
     return c;
