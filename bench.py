@@ -213,6 +213,12 @@ def bench_other_configs(torch, kc, wl):
     """Configurations 3 and 5 (decode HBM rate, prefill MFMA rate), HIP-graph replays."""
     dev = torch.device("cuda:0")
     res = {}
+    c1 = wl.config1()
+    q1, bt1, sl1 = c1.q.to(dev), c1.block_table.to(dev), c1.seq_lens.to(dev)
+    kp1, vp1 = c1.k_pool.to(dev), c1.v_pool.to(dev)
+    o1 = torch.empty_like(q1)
+    us1 = _graph_us(torch, lambda i: kc.paged_decode(q1, kp1, vp1, bt1, sl1, c1.max_seq_len, out=o1), 50)
+    res["cfg1_decode"] = {"us": round(us1, 2), "GBps": round(wl.decode_bytes(c1) / (us1 * 1e-6) / 1e9, 1)}
     c3 = wl.config3()
     pools = [wl.device_pools(c3.k_pool.shape[0], 2, 64, torch.float16, 30 + i, dev) for i in range(2)]
     q, bt, sl = c3.q.to(dev), c3.block_table.to(dev), c3.seq_lens.to(dev)
