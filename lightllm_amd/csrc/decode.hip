@@ -457,8 +457,9 @@ int balanced_wgs(DecodeFn fn, int64_t page_units_bound) {
 // Automatic schedule.  With few (sequence, kv head) units against the
 // resident work-group count, fixed splits of each unit fill the GPU in one
 // pass (S ~ resident / units, or 0.8 x that when the longest sequence gives
-// each wave more than kShortChainPages pages); with many units (a large batch
-// of uneven lengths) the balanced schedule shares the pages equally instead.
+// each wave more than kShortChainPages pages), and at most one split per 4
+// pages; with many units (a large batch of uneven lengths) the balanced
+// schedule shares the pages equally instead.
 constexpr int kAutoMaxSplits = 64;
 constexpr int kShortChainPages = 4;   // pages per wave up to which a split is latency-bound
 
@@ -480,7 +481,9 @@ AutoChoice auto_schedule(const Kernels& ks, int B, int Hkv, int max_pages) {
     // the chains are long (bandwidth-bound: extra work-groups only contend).
     int64_t S = (cap + units - 1) / units;
     if ((int64_t)max_pages > S * kDecodeWaves * kShortChainPages) S = (cap * 4 / 5 + units - 1) / units;
-    S = std::max<int64_t>(1, std::min<int64_t>({S, (int64_t)kAutoMaxSplits, (int64_t)std::max(1, max_pages)}));
+    // at least one page per wave of a split (smaller splits only add partials to merge)
+    const int64_t by_pages = (std::max(1, max_pages) + kDecodeWaves - 1) / kDecodeWaves;
+    S = std::max<int64_t>(1, std::min<int64_t>({S, (int64_t)kAutoMaxSplits, by_pages}));
     c.splits = (int)S;
     return c;
 }
