@@ -42,7 +42,7 @@ struct MfmaPrefillArgs {
     int max_blocks, N, Hq, Hkv, causal;
     float scale_log2;
     int qblocks;      // query blocks per sequence
-    int max_chunks;   // key chunks per (sequence, query block); grid.y = N * qblocks * max_chunks
+    int max_chunks;   // key chunks per (sequence, query block)
     int chunk_tiles;  // key tiles per chunk
     int groups;       // N * qblocks * max_chunks * Hkv (chunk slot, kv head) work items
     float* part_o;    // [N*qblocks*max_chunks*Hq][BQ][D] (max_chunks > 1)
