@@ -1,9 +1,10 @@
 // Paged prefill attention (varlen, causal or not) and batched first prefill
 // over contiguous K/V, for gfx950.
 //
-// Two kernels:
-//  * prefill_mfma_kernel (prefill_mfma.h): fp16/bf16, head_dim 64/128,
-//    16-token pages -- MFMA QK^T and PV tiles; the fast path.
+// Kernels:
+//  * prefill_mfma_kernel / prefill_f32_kernel (prefill_mfma.hip): fp16/bf16
+//    and fp32, head_dim 64/128, 16-token pages -- MFMA QK^T and PV tiles; the
+//    fast path.
 //  * rows_generic_kernel (this file): any dtype, any head_dim <= 256, any
 //    page size, paged or contiguous K/V.  One wave per (query row, q_head),
 //    64 keys per iteration with one key per lane, then the probabilities are

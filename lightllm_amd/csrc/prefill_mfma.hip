@@ -124,6 +124,59 @@ constexpr int kPageWindow = 256;   // page ids staged in LDS at a time
 constexpr int kXcds = 8;   // XCDs of an MI355X; work-groups go to them round-robin
 
 
+// One work-group's work item, from its blockIdx.
+//
+// Work: Y = N x qblocks x max_chunks ranked chunk slots (blockIdx-independent
+// order: slot / max_chunks is a rank in the descending order of the units'
+// key tiles, longest-processing-time first) times Hkv kv-head groups of G
+// q heads, which read the same K/V tiles.  The dispatcher hands consecutive
+// work-groups to the 8 XCDs in turn, and each XCD has its own L2, so group
+// j (slot-major) goes to XCD j % 8 with its G heads as that XCD's next G
+// work-groups: they run together and share their K/V reads in one L2.
+struct Work {
+    int hq, kvh, unit, n, ci, q0, P, q_lo, L, kend, t_begin, t_end;
+    bool direct;   // one chunk: write the output row itself
+};
+
+// False when the work-group has nothing to do (uniform over the work-group;
+// it may return before or after the ranking barriers, never between).
+__device__ inline bool take_work(const MfmaPrefillArgs& a, int* order, Work& wk) {
+    const int G = a.Hq / a.Hkv;
+#if LLKV_PREFILL_XCD
+    const int xcd = blockIdx.x % kXcds, r = blockIdx.x / kXcds;
+    const int j = (r / G) * kXcds + xcd;
+    if (j >= a.groups) return false;
+    wk.kvh = j % a.Hkv;
+    wk.hq = wk.kvh * G + r % G;
+    const int y = j / a.Hkv;
+#else
+    wk.hq = blockIdx.x % a.Hq;
+    wk.kvh = wk.hq / G;
+    const int y = blockIdx.x / a.Hq;
+    if (y * a.Hkv >= a.groups) return false;
+#endif
+    const int slot = y / a.max_chunks;
+    wk.ci = y - slot * a.max_chunks;   // key chunk of the unit
+    UnitInfo ui;
+    wk.unit = unit_by_rank(a, slot, order, ui);  // (sequence, query block)
+    wk.n = wk.unit / a.qblocks;
+    const int qb = a.qblocks - 1 - (wk.unit % a.qblocks);
+    wk.q0 = ui.q0;
+    wk.P = ui.P;
+    wk.q_lo = qb * BQ;
+    if (wk.q_lo >= wk.P) return false;
+    wk.L = ui.L;
+    int kend = a.causal ? wk.L - wk.P + min(wk.q_lo + BQ, wk.P) : wk.L;
+    wk.kend = kend < 0 ? 0 : (kend > wk.L ? wk.L : kend);
+    const int ntiles = (wk.kend + BN - 1) / BN;
+    const int nchunks = (ntiles + a.chunk_tiles - 1) / a.chunk_tiles;
+    if (wk.ci > 0 && wk.ci >= nchunks) return false;   // chunk 0 also covers an empty key range (zeros)
+    wk.t_begin = wk.ci * a.chunk_tiles;
+    wk.t_end = min(wk.t_begin + a.chunk_tiles, ntiles);
+    wk.direct = nchunks <= 1;
+    return true;
+}
+
 template <int D>
 struct Smem {
     static constexpr int KPAD = D + 8;    // halves per K row (pad: spread LDS banks)
@@ -152,47 +205,12 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, known uniform
     const int g = lane >> 4, c16 = lane & 15;
-    // Work: Y = N x qblocks x max_chunks ranked chunk slots (blockIdx-independent
-    // order: slot / max_chunks is a rank in the descending order of the units'
-    // key tiles, longest-processing-time first) times Hkv kv-head groups of G
-    // q heads, which read the same K/V tiles.  The dispatcher hands consecutive
-    // work-groups to the 8 XCDs in turn, and each XCD has its own L2, so group
-    // j (slot-major) goes to XCD j % 8 with its G heads as that XCD's next G
-    // work-groups: they run together and share their K/V reads in one L2.
-    const int G = a.Hq / a.Hkv;
-#if LLKV_PREFILL_XCD
-    const int xcd = blockIdx.x % kXcds, r = blockIdx.x / kXcds;
-    const int j = (r / G) * kXcds + xcd;
-    if (j >= a.groups) return;
-    const int kvh = j % a.Hkv;
-    const int hq = kvh * G + r % G;
-    const int y = j / a.Hkv;
-#else
-    const int hq = blockIdx.x % a.Hq;
-    const int kvh = hq / G;
-    const int y = blockIdx.x / a.Hq;
-    if (y * a.Hkv >= a.groups) return;
-#endif
-    const int slot = y / a.max_chunks;
-    const int ci = y - slot * a.max_chunks;   // key chunk of the unit
-    UnitInfo ui;
-    const int unit = unit_by_rank(a, slot, sm.order, ui);  // (sequence, query block)
-    const int n = unit / a.qblocks;
-    const int qb = a.qblocks - 1 - (unit % a.qblocks);
-
-    const int q0 = ui.q0;
-    const int P = ui.P;
-    const int q_lo = qb * BQ;
-    if (q_lo >= P) return;
-    const int L = ui.L;
-    int kend = a.causal ? L - P + min(q_lo + BQ, P) : L;
-    kend = kend < 0 ? 0 : (kend > L ? L : kend);
-    const int ntiles = (kend + BN - 1) / BN;
-    const int nchunks = (ntiles + a.chunk_tiles - 1) / a.chunk_tiles;
-    if (ci > 0 && ci >= nchunks) return;   // chunk 0 also covers an empty key range (zeros)
-    const int t_begin = ci * a.chunk_tiles;
-    const int t_end = min(t_begin + a.chunk_tiles, ntiles);
-    const bool direct = nchunks <= 1;
+    Work wk;
+    if (!take_work(a, sm.order, wk)) return;
+    const int hq = wk.hq, kvh = wk.kvh, unit = wk.unit, n = wk.n, ci = wk.ci;
+    const int q0 = wk.q0, P = wk.P, q_lo = wk.q_lo, L = wk.L, kend = wk.kend;
+    const int t_begin = wk.t_begin, t_end = wk.t_end;
+    const bool direct = wk.direct;
     const int last_page = L > 0 ? (L - 1) / kPage : 0;
     const int* bt = a.bt + (int64_t)n * a.max_blocks;
     const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)kvh * D;
@@ -416,17 +434,6 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 pop[ss][nt].w = Mfma<T>::pack2(pv[1][2], pv[1][3]);
             }
         };
-        auto pv_half = [&](int ss) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const uint4 va = *reinterpret_cast<const uint4*>(
-                    &sm.vt[buf][(dt * 16 + c16) * VPAD + 32 * ss + 8 * g]);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) o[dt][nt] = Mfma<T>::mma(va, pop[ss][nt], o[dt][nt]);
-            }
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) osum[nt] = Mfma<T>::mma(ones, pop[ss][nt], osum[nt]);
-        };
 #if LLKV_PREFILL_INTERLEAVE
         // The first half's MFMAs, each followed by a share of the second half's
         // exponentials; sched_barrier keeps this order (the scheduler would
@@ -475,6 +482,17 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             for (int nt = 0; nt < 2; ++nt) osum[nt] = Mfma<T>::mma(ones, pop[1][nt], osum[nt]);
         }
 #else
+        auto pv_half = [&](int ss) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const uint4 va = *reinterpret_cast<const uint4*>(
+                    &sm.vt[buf][(dt * 16 + c16) * VPAD + 32 * ss + 8 * g]);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) o[dt][nt] = Mfma<T>::mma(va, pop[ss][nt], o[dt][nt]);
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) osum[nt] = Mfma<T>::mma(ones, pop[ss][nt], osum[nt]);
+        };
         softmax_half(0);
         pv_half(0);
         softmax_half(1);
@@ -516,6 +534,301 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             if (g == 0) a.part_lse[pidx * BQ + row] = lt > 0.f ? m[nt] + fast_log2(lt) : -INFINITY;
         }
     }
+}
+
+// fp32 pools: v_mfma_f32_16x16x4f32 for both products, same work mapping,
+// chunking and merge as the 16-bit kernel.  Per wave and 64-key tile:
+//   S^T = K Q^T   A = K rows from LDS, one 16-byte read feeds four k-steps:
+//                 lane (g, c16) holds dims 16kb + 4g .. 16kb + 4g + 3 of key
+//                 row c16, and Q^T (registers) holds the same dims of query
+//                 c16, so k-step j of block kb contracts dim 16kb + 4g + j.
+//                 Accumulator lane (g, c16) holds keys 4g + i of query c16.
+//   O^T = V^T P^T the lane's four keys 4g + i of a 16-key tile are exactly the
+//                 k-slot g of four k-steps (i = 0..3), so P^T never leaves
+//                 registers; A = V^T (transposed while staging) read 16 bytes
+//                 (keys 4g .. 4g + 3 of one dim) per four k-steps.
+// Softmax row sums are kept per lane (its own keys) and reduced over the four
+// lanes of a query column at the end.  LDS holds one K / V^T tile pair for
+// head_dim 128 (two for 64), so that two work-groups fit on a CU.
+template <int D>
+struct SmemF32 {
+    static constexpr int NB = D == 64 ? 2 : 1;   // LDS tile buffers
+    static constexpr int KPAD = D + 4;    // floats per K row (pad: 16-byte reads of 16 rows hit distinct banks)
+    static constexpr int VPAD = BN + 4;   // floats per V^T row
+    union {
+        struct {
+            alignas(16) float k[NB][BN * KPAD];
+            alignas(16) float vt[NB][D * VPAD];
+        };
+        int order[5 * kRankUnits];
+    };
+    int pages[kPageWindow];
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_f32_kernel(MfmaPrefillArgs a) {
+    typedef SmemF32<D> S;
+    constexpr int KPAD = S::KPAD, VPAD = S::VPAD, NB = S::NB;
+    constexpr int KB = D / 16;              // 16-dim blocks of the QK^T product
+    constexpr int DT = D / 16;              // 16-dim tiles of the output
+    constexpr int KCH_T = BN * D / 4 / 256;          // 16-byte K chunks per thread
+    constexpr int VT_T = (BN / 4) * (D / 4) / 256;   // V tasks (4 keys x 4 dims) per thread
+    __shared__ S sm;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, c16 = lane & 15;
+    Work wk;
+    if (!take_work(a, sm.order, wk)) return;
+    const int hq = wk.hq, kvh = wk.kvh, unit = wk.unit, n = wk.n, ci = wk.ci;
+    const int q0 = wk.q0, P = wk.P, q_lo = wk.q_lo, L = wk.L, kend = wk.kend;
+    const int t_begin = wk.t_begin, t_end = wk.t_end;
+    const int last_page = L > 0 ? (L - 1) / kPage : 0;
+    const int* bt = a.bt + (int64_t)n * a.max_blocks;
+
+    float4 qop[2][KB];
+    const float* qg = reinterpret_cast<const float*>(a.q);
+    auto load_q = [&]() {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int ql = q_lo + w * WQ + nt * 16 + c16;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+                qop[nt][kb] = ql < P ? *reinterpret_cast<const float4*>(
+                                           qg + ((int64_t)(q0 + ql) * a.Hq + hq) * D + kb * 16 + g * 4)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    int qpos[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const int ql = q_lo + w * WQ + nt * 16 + c16;
+        qpos[nt] = ql < P ? (a.causal ? L - P + ql : L - 1) : -1;
+    }
+    const int wq0 = q_lo + w * WQ;
+    const int wave_min_pos = (wq0 + WQ <= P) ? (a.causal ? L - P + wq0 : L - 1) : -1;
+
+    f32x4 o[DT][2];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) o[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m[2] = {kNegBig, kNegBig};
+    float lsum[2] = {0.f, 0.f};   // this lane's keys only
+
+    int tbase = 0;
+    u32x4 kr[KCH_T];
+    u32x4 vr[VT_T][4];
+    const uint32_t row_bytes = (uint32_t)(a.Hkv * D * sizeof(float));
+    const uint32_t page_bytes = row_bytes * kPage;
+    const char* kb_ = reinterpret_cast<const char*>(reinterpret_cast<const float*>(a.k) + (int64_t)kvh * D);
+    const char* vb_ = reinterpret_cast<const char*>(reinterpret_cast<const float*>(a.v) + (int64_t)kvh * D);
+    uint32_t koff[KCH_T], voff[VT_T];
+    int kslot[KCH_T], vslot[VT_T];
+#pragma unroll
+    for (int j = 0; j < KCH_T; ++j) {
+        const int ch = tid + 256 * j;
+        const int key = ch / (D / 4), c = ch % (D / 4);
+        kslot[j] = key >> 4;
+        koff[j] = (uint32_t)(key & 15) * row_bytes + (uint32_t)c * 16u;
+    }
+#pragma unroll
+    for (int j = 0; j < VT_T; ++j) {
+        const int task = tid + 256 * j;
+        const int kq = task % (BN / 4), c = task / (BN / 4);   // keys 4kq .. 4kq+3, dims 4c .. 4c+3
+        vslot[j] = (4 * kq) >> 4;
+        voff[j] = (uint32_t)((4 * kq) & 15) * row_bytes + (uint32_t)c * 16u;
+    }
+    auto load_tile = [&](int t) {
+        const int* pg = sm.pages + (4 * t - tbase);
+#pragma unroll
+        for (int j = 0; j < KCH_T; ++j) {
+            const uint64_t phys = (uint32_t)max(pg[kslot[j]], 0);
+            kr[j] = *reinterpret_cast<const u32x4*>(kb_ + phys * page_bytes + koff[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < VT_T; ++j) {
+            const uint64_t phys = (uint32_t)max(pg[vslot[j]], 0);
+            const char* p = vb_ + phys * page_bytes + voff[j];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) vr[j][r] = *reinterpret_cast<const u32x4*>(p + r * row_bytes);
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < KCH_T; ++j) {
+            const int ch = tid + 256 * j;
+            const int key = ch / (D / 4), c = ch % (D / 4);
+            *reinterpret_cast<u32x4*>(&sm.k[buf][key * KPAD + c * 4]) = kr[j];
+        }
+#pragma unroll
+        for (int j = 0; j < VT_T; ++j) {
+            const int task = tid + 256 * j;
+            const int kq = task % (BN / 4), c = task / (BN / 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)   // 4x4 transpose: V^T row 4c + e, keys 4kq .. 4kq+3
+                *reinterpret_cast<u32x4*>(&sm.vt[buf][(4 * c + e) * VPAD + 4 * kq]) =
+                    u32x4{vr[j][0][e], vr[j][1][e], vr[j][2][e], vr[j][3][e]};
+        }
+    };
+    auto stage_pages = [&](int base) {
+        tbase = base;
+        for (int i = tid; i < kPageWindow; i += 256) sm.pages[i] = bt[min(base + i, last_page)];
+        lds_barrier();
+    };
+    if (t_begin < t_end) {
+        stage_pages(4 * t_begin);
+        load_q();
+        load_tile(t_begin);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    for (int t = t_begin; t < t_end; ++t) {
+        const int buf = NB == 2 ? (t - t_begin) & 1 : 0;
+        if (t + 1 < t_end) {
+            if (4 * (t + 1) + 4 > tbase + kPageWindow) stage_pages(4 * (t + 1));
+            load_tile(t + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- S^T = K Q^T: key tile kt holds keys 16kt .. 16kt+15 ---------
+        // The two halves of the head dims accumulate apart and are added at
+        // the end: half the rounding steps in each sum, which halves the
+        // score's rounding error (it dominates the fp32 output's error).
+        f32x4 s[4][2];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            f32x4 hi[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                s[kt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                hi[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const float4 ka = *reinterpret_cast<const float4*>(
+                    &sm.k[buf][(16 * kt + c16) * KPAD + kb * 16 + g * 4]);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    f32x4& acc = kb < KB / 2 ? s[kt][nt] : hi[nt];
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.x, qop[nt][kb].x, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.y, qop[nt][kb].y, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.z, qop[nt][kb].z, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.w, qop[nt][kb].w, acc, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) s[kt][nt] += hi[nt];
+        }
+
+        // ---- mask and online softmax (scores scaled in the exponent) -----
+        const int key0 = t * BN;
+        const float c = a.scale_log2;
+        const bool unmasked = key0 + BN - 1 <= wave_min_pos && key0 + BN <= kend;
+        float mx[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            if (!unmasked) {
+                // key = key0 + 16kt + 4g + i is visible iff key <= min(qpos, kend - 1)
+                const int r = min(qpos[nt], kend - 1) - key0 - 4 * g;
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (16 * kt + i > r) s[kt][nt][i] = -INFINITY;
+            }
+            float v = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v = fmaxf(v, s[kt][nt][i]);
+            mx[nt] = v * c;
+        }
+        bool grow = false;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) grow |= mx[nt] > m[nt] + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                float v = mx[nt];
+                v = fmaxf(v, __shfl_xor(v, 16, 64));
+                v = fmaxf(v, __shfl_xor(v, 32, 64));
+                const float mnew = fmaxf(m[nt], v);
+                const float corr = fast_exp2(m[nt] - mnew);
+                m[nt] = mnew;
+                lsum[nt] *= corr;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o[dt][nt] *= corr;
+            }
+        }
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = fast_exp2(fmaf(s[kt][nt][i], c, -m[nt]));
+                    s[kt][nt][i] = p;
+                    lsum[nt] += p;
+                }
+
+        // ---- O^T += V^T P^T ------------------------------------------------
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const float4 va = *reinterpret_cast<const float4*>(
+                    &sm.vt[buf][(dt * 16 + c16) * VPAD + 16 * kt + 4 * g]);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.x, s[kt][nt][0], o[dt][nt], 0, 0, 0);
+                    o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.y, s[kt][nt][1], o[dt][nt], 0, 0, 0);
+                    o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.z, s[kt][nt][2], o[dt][nt], 0, 0, 0);
+                    o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.w, s[kt][nt][3], o[dt][nt], 0, 0, 0);
+                }
+            }
+
+        if (t + 1 < t_end) {
+            if (NB == 1) __syncthreads();   // every wave is done with the single buffer
+            store_tile(NB == 2 ? buf ^ 1 : 0);
+        }
+        __syncthreads();
+    }
+
+    float* og = reinterpret_cast<float*>(a.out);
+    const int64_t pidx = ((int64_t)unit * a.max_chunks + ci) * a.Hq + hq;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        float lt = lsum[nt];
+        lt += __shfl_xor(lt, 16, 64);
+        lt += __shfl_xor(lt, 32, 64);
+        const int row = w * WQ + nt * 16 + c16;
+        const int ql = q_lo + row;
+        if (ql >= P) continue;
+        const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+        float* dst = wk.direct ? og + ((int64_t)(q0 + ql) * a.Hq + hq) * D
+                               : a.part_o + (pidx * BQ + row) * D;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+            *reinterpret_cast<float4*>(dst + dt * 16 + 4 * g) =
+                make_float4(o[dt][nt][0] * inv, o[dt][nt][1] * inv, o[dt][nt][2] * inv, o[dt][nt][3] * inv);
+        if (!wk.direct && g == 0) a.part_lse[pidx * BQ + row] = lt > 0.f ? m[nt] + fast_log2(lt) : -INFINITY;
+    }
+}
+
+// Four consecutive output elements from fp32 values.
+template <typename T>
+__device__ inline void store4(T* p, float x, float y, float z, float w) {
+    uint2 w2;
+    w2.x = Mfma<T>::pack2(x, y);
+    w2.y = Mfma<T>::pack2(z, w);
+    *reinterpret_cast<uint2*>(p) = w2;
+}
+template <>
+__device__ inline void store4<float>(float* p, float x, float y, float z, float w) {
+    *reinterpret_cast<float4*>(p) = make_float4(x, y, z, w);
 }
 
 // Merge of a (sequence, query block, q head) unit's key chunks: grid
@@ -570,17 +883,12 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
     const float inv = W > 0.f ? 1.0f / W : 0.f;
     T* orow = reinterpret_cast<T*>(a.out) + ((int64_t)(q0 + q_lo + row) * a.Hq + hq) * D + part * V4 * 4;
 #pragma unroll
-    for (int v = 0; v < V4; ++v) {
-        uint2 w2;
-        w2.x = Mfma<T>::pack2(acc[v].x * inv, acc[v].y * inv);
-        w2.y = Mfma<T>::pack2(acc[v].z * inv, acc[v].w * inv);
-        *reinterpret_cast<uint2*>(orow + 4 * v) = w2;
-    }
+    for (int v = 0; v < V4; ++v)
+        store4(orow + 4 * v, acc[v].x * inv, acc[v].y * inv, acc[v].z * inv, acc[v].w * inv);
 }
 
 bool prefill_mfma_handles(int head_dim, int block_size, int dtype) {
-    return block_size == kPage && (dtype == LLKV_DTYPE_F16 || dtype == LLKV_DTYPE_BF16) &&
-           (head_dim == 64 || head_dim == 128);
+    return block_size == kPage && (head_dim == 64 || head_dim == 128);
 }
 
 // Key-range split.  When the (sequence, query block, q head) units alone
@@ -600,6 +908,9 @@ constexpr int kMinChunkTiles = 8;
 constexpr int kSizingSlots = 1024;
 
 const void* prefill_kernel_fn(int dtype, int head_dim) {
+    if (dtype == LLKV_DTYPE_F32)
+        return head_dim == 64 ? reinterpret_cast<const void*>(prefill_f32_kernel<64>)
+                              : reinterpret_cast<const void*>(prefill_f32_kernel<128>);
     if (dtype == LLKV_DTYPE_F16)
         return head_dim == 64 ? reinterpret_cast<const void*>(prefill_mfma_kernel<_Float16, 64>)
                               : reinterpret_cast<const void*>(prefill_mfma_kernel<_Float16, 128>);
@@ -671,7 +982,15 @@ int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dty
     dim3 grid((unsigned)(((a.groups + kXcds - 1) / kXcds) * kXcds * G));
     dim3 mgrid(a.Hq, a.N * a.qblocks);
     const bool merge = a.max_chunks > 1;
-    if (dtype == LLKV_DTYPE_F16) {
+    if (dtype == LLKV_DTYPE_F32) {
+        if (head_dim == 64) {
+            prefill_f32_kernel<64><<<grid, 256, 0, st>>>(a);
+            if (merge) prefill_merge_kernel<float, 64><<<mgrid, 256, 0, st>>>(a);
+        } else {
+            prefill_f32_kernel<128><<<grid, 256, 0, st>>>(a);
+            if (merge) prefill_merge_kernel<float, 128><<<mgrid, 256, 0, st>>>(a);
+        }
+    } else if (dtype == LLKV_DTYPE_F16) {
         if (head_dim == 64) {
             prefill_mfma_kernel<_Float16, 64><<<grid, 256, 0, st>>>(a);
             if (merge) prefill_merge_kernel<_Float16, 64><<<mgrid, 256, 0, st>>>(a);

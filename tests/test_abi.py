@@ -136,8 +136,11 @@ def test_prefill_workspace_size():
     # configuration 4 (keys up to 4608): chunked, fp32 partials of 128 rows x (D + 1)
     n = ws(8, 4096, 512, 4608, 14, 64, 16, 1)
     assert n > 0 and n % (128 * 65 * 4) == 0
-    # fp32 pools use the generic kernel: no workspace
-    assert ws(8, 4096, 512, 4608, 14, 64, 16, 0) == 0
+    # fp32 pools take the same plan (same fp32 partials)
+    assert ws(8, 4096, 512, 4608, 14, 64, 16, 0) == n
+    # shapes outside the MFMA kernels (head_dim 67, page size 8) run unsplit: no workspace
+    assert ws(8, 4096, 512, 4608, 14, 67, 16, 0) == 0
+    assert ws(8, 4096, 512, 4608, 14, 64, 8, 1) == 0
 
 
 def test_hash_tokens_abi():

@@ -549,6 +549,12 @@ PREFILL = [
     ("fp16_D64_long_noncausal", 14, 2, 64, [3000], [100], torch.float16, False),
     ("bf16_D64_long", 14, 2, 64, [2500, 0], [300, 40], torch.bfloat16, True),
     ("fp16_D128_long", 32, 8, 128, [2100], [130], torch.float16, True),
+    # fp32 MFMA kernel (16x16x4 f32): head_dim 64 and 128, split and unsplit, masks
+    ("fp32_D128", 32, 8, 128, [0, 1000], [256, 77], torch.float32, True),
+    ("fp32_D128_noncausal", 32, 8, 128, [40], [150], torch.float32, False),
+    ("fp32_mha", 4, 4, 64, [31], [97], torch.float32, True),
+    ("fp32_D64_long", 14, 2, 64, [2500, 0], [300, 40], torch.float32, True),
+    ("fp32_D128_long", 32, 8, 128, [2100], [130], torch.float32, True),
 ]
 
 
@@ -572,7 +578,7 @@ def test_prefill_cases(name, hq, hkv, d, prefixes, chunks, dtype, causal):
         check_lowp(out, ref, name, 2e-3 if dtype == torch.float16 else 1.6e-2)
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_prefill_loose_bounds(dtype):
     """Host bounds far above the actual lengths (more key chunks and query blocks planned than
     the sequences use): the extra work-groups find nothing to do and the result is unchanged."""
@@ -588,6 +594,10 @@ def test_prefill_loose_bounds(dtype):
                              scale=case.scale)
     torch.cuda.synchronize()
     ref = oracle_prefill(case, kp, vp)
+    if dtype == torch.float32:
+        check_fp32(loose, ref, "prefill loose bounds")
+        check_fp32(tight, ref, "prefill tight bounds")
+        return
     check_lowp(loose, ref, "prefill loose bounds", 2e-3 if dtype == torch.float16 else 1.6e-2)
     check_lowp(tight, ref, "prefill tight bounds", 2e-3 if dtype == torch.float16 else 1.6e-2)
 
