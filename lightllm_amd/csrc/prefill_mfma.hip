@@ -548,17 +548,39 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 //                 registers; A = V^T (transposed while staging) read 16 bytes
 //                 (keys 4g .. 4g + 3 of one dim) per four k-steps.
 // Softmax row sums are kept per lane (its own keys) and reduced over the four
-// lanes of a query column at the end.  LDS holds one K / V^T tile pair for
-// head_dim 128 (two for 64), so that two work-groups fit on a CU.
+// lanes of a query column at the end.
+// LDS tile buffers and occupancy.  head_dim 64: K double-buffered, V^T
+// single (53 KB), three waves per SIMD (the compiler spills ~60 registers to
+// reach 168; still 13 % faster than two waves without spills).  head_dim 128:
+// ~300 registers, one wave per SIMD, so both tiles double-buffered (137 KB).
+#ifndef LLKV_F32_KNB64
+#define LLKV_F32_KNB64 2
+#endif
+#ifndef LLKV_F32_VNB64
+#define LLKV_F32_VNB64 1
+#endif
+#ifndef LLKV_F32_WPE64
+#define LLKV_F32_WPE64 3
+#endif
+#ifndef LLKV_F32_WPE128
+#define LLKV_F32_WPE128 1
+#endif
+#ifndef LLKV_F32_KNB128
+#define LLKV_F32_KNB128 2
+#endif
+#ifndef LLKV_F32_VNB128
+#define LLKV_F32_VNB128 2
+#endif
 template <int D>
 struct SmemF32 {
-    static constexpr int NB = D == 64 ? 2 : 1;   // LDS tile buffers
+    static constexpr int KNB = D == 64 ? LLKV_F32_KNB64 : LLKV_F32_KNB128;
+    static constexpr int VNB = D == 64 ? LLKV_F32_VNB64 : LLKV_F32_VNB128;
     static constexpr int KPAD = D + 4;    // floats per K row (pad: 16-byte reads of 16 rows hit distinct banks)
     static constexpr int VPAD = BN + 4;   // floats per V^T row
     union {
         struct {
-            alignas(16) float k[NB][BN * KPAD];
-            alignas(16) float vt[NB][D * VPAD];
+            alignas(16) float k[KNB][BN * KPAD];
+            alignas(16) float vt[VNB][D * VPAD];
         };
         int order[5 * kRankUnits];
     };
@@ -566,9 +588,10 @@ struct SmemF32 {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void prefill_f32_kernel(MfmaPrefillArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? LLKV_F32_WPE64 : LLKV_F32_WPE128)))
+void prefill_f32_kernel(MfmaPrefillArgs a) {
     typedef SmemF32<D> S;
-    constexpr int KPAD = S::KPAD, VPAD = S::VPAD, NB = S::NB;
+    constexpr int KPAD = S::KPAD, VPAD = S::VPAD, KNB = S::KNB, VNB = S::VNB;
     constexpr int KB = D / 16;              // 16-dim blocks of the QK^T product
     constexpr int DT = D / 16;              // 16-dim tiles of the output
     constexpr int KCH_T = BN * D / 4 / 256;          // 16-byte K chunks per thread
@@ -640,13 +663,18 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(MfmaPrefillArgs a) {
         vslot[j] = (4 * kq) >> 4;
         voff[j] = (uint32_t)((4 * kq) & 15) * row_bytes + (uint32_t)c * 16u;
     }
-    auto load_tile = [&](int t) {
+    // Next-tile staging in two halves (K, then V^T), so that only one half's
+    // registers are live at a time.
+    auto load_k = [&](int t) {
         const int* pg = sm.pages + (4 * t - tbase);
 #pragma unroll
         for (int j = 0; j < KCH_T; ++j) {
             const uint64_t phys = (uint32_t)max(pg[kslot[j]], 0);
             kr[j] = *reinterpret_cast<const u32x4*>(kb_ + phys * page_bytes + koff[j]);
         }
+    };
+    auto load_v = [&](int t) {
+        const int* pg = sm.pages + (4 * t - tbase);
 #pragma unroll
         for (int j = 0; j < VT_T; ++j) {
             const uint64_t phys = (uint32_t)max(pg[vslot[j]], 0);
@@ -655,13 +683,15 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(MfmaPrefillArgs a) {
             for (int r = 0; r < 4; ++r) vr[j][r] = *reinterpret_cast<const u32x4*>(p + r * row_bytes);
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_k = [&](int buf) {
 #pragma unroll
         for (int j = 0; j < KCH_T; ++j) {
             const int ch = tid + 256 * j;
             const int key = ch / (D / 4), c = ch % (D / 4);
             *reinterpret_cast<u32x4*>(&sm.k[buf][key * KPAD + c * 4]) = kr[j];
         }
+    };
+    auto store_v = [&](int buf) {
 #pragma unroll
         for (int j = 0; j < VT_T; ++j) {
             const int task = tid + 256 * j;
@@ -680,16 +710,20 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(MfmaPrefillArgs a) {
     if (t_begin < t_end) {
         stage_pages(4 * t_begin);
         load_q();
-        load_tile(t_begin);
-        store_tile(0);
+        load_k(t_begin);
+        load_v(t_begin);
+        store_k(0);
+        store_v(0);
     }
     __syncthreads();
 
     for (int t = t_begin; t < t_end; ++t) {
-        const int buf = NB == 2 ? (t - t_begin) & 1 : 0;
-        if (t + 1 < t_end) {
+        const int kbuf = KNB == 2 ? (t - t_begin) & 1 : 0;
+        const int vbuf = VNB == 2 ? (t - t_begin) & 1 : 0;
+        const bool next = t + 1 < t_end;   // uniform
+        if (next) {
             if (4 * (t + 1) + 4 > tbase + kPageWindow) stage_pages(4 * (t + 1));
-            load_tile(t + 1);
+            load_k(t + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
 
@@ -709,7 +743,7 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(MfmaPrefillArgs a) {
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
                 const float4 ka = *reinterpret_cast<const float4*>(
-                    &sm.k[buf][(16 * kt + c16) * KPAD + kb * 16 + g * 4]);
+                    &sm.k[kbuf][(16 * kt + c16) * KPAD + kb * 16 + g * 4]);
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
                     f32x4& acc = kb < KB / 2 ? s[kt][nt] : hi[nt];
@@ -721,6 +755,11 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(MfmaPrefillArgs a) {
             }
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) s[kt][nt] += hi[nt];
+        }
+        if (next) {
+            if (KNB == 1) __syncthreads();   // every wave is done with the K buffer
+            store_k(KNB == 2 ? kbuf ^ 1 : 0);
+            load_v(t + 1);
         }
 
         // ---- mask and online softmax (scores scaled in the exponent) -----
@@ -776,11 +815,11 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(MfmaPrefillArgs a) {
 
         // ---- O^T += V^T P^T ------------------------------------------------
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 const float4 va = *reinterpret_cast<const float4*>(
-                    &sm.vt[buf][(dt * 16 + c16) * VPAD + 16 * kt + 4 * g]);
+                    &sm.vt[vbuf][(dt * 16 + c16) * VPAD + 16 * kt + 4 * g]);
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
                     o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.x, s[kt][nt][0], o[dt][nt], 0, 0, 0);
@@ -789,10 +828,11 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(MfmaPrefillArgs a) {
                     o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.w, s[kt][nt][3], o[dt][nt], 0, 0, 0);
                 }
             }
+        }
 
-        if (t + 1 < t_end) {
-            if (NB == 1) __syncthreads();   // every wave is done with the single buffer
-            store_tile(NB == 2 ? buf ^ 1 : 0);
+        if (next) {
+            if (VNB == 1) __syncthreads();   // every wave is done with the V^T buffer
+            store_v(VNB == 2 ? vbuf ^ 1 : 0);
         }
         __syncthreads();
     }
