@@ -46,6 +46,7 @@ HBM_PEAK_GBS = 8000.0
 COPY_CAL_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_cfg2_traffic.txt")
 FP16_MFMA_PEAK_TFLOPS = 2500.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
 METRIC = "paged decode µs/layer + achieved HBM GB/s (% peak) at B=64; prefill MFMA %"
 
 
@@ -165,9 +166,9 @@ def bench_decode(args, torch, kc, wl):
     }
 
 
-def bench_prefill(args, torch, kc, wl):
+def bench_prefill(args, torch, kc, wl, dtype=None):
     dev = torch.device("cuda:0")
-    case = wl.config4()
+    case = wl.config4() if dtype is None else wl.config4(dtype=dtype)
     kp, vp = case.k_pool.to(dev), case.v_pool.to(dev)
     kc.append_kv(case.k_chunk.to(dev), case.v_chunk.to(dev), case.slots.to(dev), kp, vp)
     q = case.q.to(dev)
@@ -181,7 +182,8 @@ def bench_prefill(args, torch, kc, wl):
     us = _graph_us(torch, lambda i: run(), max(20, args.steps // 4))
     flops = wl.prefill_flops(case)
     tflops = flops / (us * 1e-6) / 1e12
-    return {"us": us, "flop": flops, "tflops": tflops, "mfma_frac": tflops / FP16_MFMA_PEAK_TFLOPS}
+    peak = FP32_MFMA_PEAK_TFLOPS if case.q.dtype == torch.float32 else FP16_MFMA_PEAK_TFLOPS
+    return {"us": us, "flop": flops, "tflops": tflops, "mfma_frac": tflops / peak}
 
 
 def _graph_us(torch, fn, n, warm_replays=3, timed_replays=5):
@@ -538,6 +540,9 @@ def main():
     if pre is not None:
         line["prefill_cfg4"] = {"us": round(pre["us"], 2), "TFLOPs": round(pre["tflops"], 1),
                                 "mfma_frac": round(pre["mfma_frac"], 4), "flop": pre["flop"]}
+        pre32 = bench_prefill(args, torch, kc, wl, dtype=torch.float32)
+        line["prefill_cfg4_shape_fp32"] = {"us": round(pre32["us"], 2), "TFLOPs": round(pre32["tflops"], 1),
+                                           "mfma_frac_of_fp32_peak": round(pre32["mfma_frac"], 4)}
     if other is not None:
         line["other_configs"] = other
     print(json.dumps(line), flush=True)

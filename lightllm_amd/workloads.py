@@ -185,11 +185,12 @@ def prefill_case(name: str, hq: int, hkv: int, d: int, prefixes: List[int], chun
 CFG4_PREFIXES = [0, 256, 1024, 4096, 4096, 4096, 2048, 512]
 
 
-def config4(seed: int = 4, nb: int = 4096) -> PrefillCase:
+def config4(seed: int = 4, nb: int = 4096, dtype=torch.float16) -> PrefillCase:
     """8 x 512-token chunks over prefixes {0,256,1024,4096,4096,4096,2048,512}; the three 4096
-    prefixes share physical pages; causal; 14/2/64 fp16."""
+    prefixes share physical pages; causal; 14/2/64 fp16 (dtype: the same shape in another
+    element type)."""
     return prefill_case("cfg4", 14, 2, 64, CFG4_PREFIXES, [512] * 8, {3: [3, 4, 5]}, nb,
-                        torch.float16, seed)
+                        dtype, seed)
 
 
 @dataclass
