@@ -32,7 +32,7 @@
 #include <utility>
 
 #include "attn_common.h"
-#include "decode_mfma.h"
+#include "decode_kernels.h"
 
 namespace llkv {
 namespace {
@@ -200,93 +200,6 @@ struct LiveWG {
     __device__ bool operator()(int j) const { return wg_nonempty(w0 + j, T, nwg); }
 };
 
-// Fixed split schedule: grid (S_max, Hkv, B), 4 waves per work-group, one
-// segment each.
-template <class Body>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Body::kWavesPerEU)))
-void decode_split_kernel(DecodeArgs a) {
-    __shared__ typename Body::Smem sm;
-    __shared__ SegDesc segs[1];
-    using T = typename Body::T;
-    LLKV_TRACE_POINT(0);
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const SplitGeo geo = split_geo(a, b);
-    const int hq0 = kvh * Body::GQ;
-    if (geo.npages == 0) {   // empty sequence: zeros, as the reference (:224-227)
-        if (split == 0) {
-            T* out = reinterpret_cast<T*>(a.out) + ((int64_t)b * a.Hq + hq0) * Body::HD;
-            for (int i = threadIdx.x; i < Body::GQ * Body::HD; i += blockDim.x)
-                out[i] = Elem<T>::from_f32(0.0f);
-        }
-        return;
-    }
-    if (split >= geo.nsplit) return;
-    if (threadIdx.x == 0) {
-        SegDesc& d = segs[0];
-        d.b = b;
-        d.kvh = kvh;
-        d.pg_begin = split * geo.pps;
-        d.npages = min(geo.pps, geo.npages - d.pg_begin);
-        d.cum = 0;
-        d.tok_end = min((d.pg_begin + d.npages) * kPage, geo.L);
-        d.direct = geo.nsplit == 1;
-        d.new_tok = seg_new_tok(a, b, d.pg_begin, d.tok_end, geo.L);
-        const int64_t bh0 = (int64_t)b * a.Hq + hq0;
-        d.po_off = (bh0 * a.S_max + split) * a.D;
-        d.pl_off = bh0 * a.S_max + split;
-    }
-    __syncthreads();
-    store_new_row<T, Body::HD>(a, segs[0]);
-    Body::round(a, sm, segs, 1, (int64_t)a.S_max * a.D, a.S_max);
-}
-
-// Balanced schedule: grid (nwg), 4 waves per work-group.  Every work-group
-// scans the lengths itself (the batch is at most kBalanceMaxB sequences) and
-// cuts its share into segments, run kSegMax segments per round.  A unit
-// (sequence, kv head) inside one share is written directly; the others are
-// merged by decode_merge_balanced_kernel.  Work-group 0 stores the page
-// prefix sums for that kernel; empty sequences get zeros from the work-group
-// with their index modulo nwg.
-template <class Body>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Body::kWavesPerEU)))
-void decode_balanced_kernel(DecodeArgs a) {
-    using T = typename Body::T;
-    constexpr int D = Body::HD;
-    __shared__ typename Body::Smem sm;
-    __shared__ int sP[kBalanceMaxB + 1];
-    __shared__ int sL[kBalanceMaxB];
-    __shared__ SegDesc segs[Body::kSegMax];
-    __shared__ int s_n;
-    __shared__ int64_t s_next;
-    LLKV_TRACE_POINT(0);
-    scan_pages(a, sP, sL);
-    LLKV_TRACE_POINT(4);
-    const int tid = threadIdx.x;
-    if (blockIdx.x == 0)
-        for (int i = tid; i <= a.B; i += blockDim.x) a.plan[i] = sP[i];
-    const int64_t T_ = (int64_t)a.Hkv * sP[a.B];
-    const int64_t wg = blockIdx.x;
-    for (int b = (int)wg; b < a.B; b += a.nwg) {   // the reference's seq_len == 0 rule (:224-227)
-        if (sP[b + 1] != sP[b]) continue;
-        T* out = reinterpret_cast<T*>(a.out) + (int64_t)b * a.Hq * D;
-        for (int i = tid; i < a.Hq * D; i += blockDim.x) out[i] = Elem<T>::from_f32(0.0f);
-    }
-    const int64_t r1 = share_begin(wg + 1, T_, a.nwg);
-    int64_t p = share_begin(wg, T_, a.nwg);
-    while (p < r1) {
-        if (tid == 0) {
-            int n = 0;
-            s_next = build_segments(a, sP, sL, p, r1, wg, Body::kSegMax, segs, &n);
-            s_n = n;
-        }
-        __syncthreads();
-        const int n = s_n;
-        p = s_next;
-        for (int i = 0; i < n; ++i) store_new_row<T, D>(a, segs[i]);
-        Body::round(a, sm, segs, n, D, 1);   // ends with a barrier
-    }
-}
-
 // Merge of the balanced schedule: grid (Hq, B), one wave each.  Unit
 // (b, kvh) spans positions [s, e); its segments are those of work-groups
 // wg_of(s) .. wg_of(e - 1), with ids w + u.
@@ -317,69 +230,11 @@ __global__ __launch_bounds__(64) void decode_merge_balanced_kernel(DecodeArgs a)
 // ---------------------------------------------------------------------------
 // Host dispatch
 // ---------------------------------------------------------------------------
-typedef void (*DecodeFn)(DecodeArgs);
-
-struct Kernels {
-    DecodeFn split = nullptr;
-    DecodeFn balanced = nullptr;
-};
-
-template <class Body>
-Kernels kernels_of() {
-    Kernels k;
-    k.split = decode_split_kernel<Body>;
-    k.balanced = decode_balanced_kernel<Body>;
-    return k;
-}
-
-template <typename T, int D, bool A>
-Kernels pick_mfma16_g(int G) {
-    switch (G) {
-        case 1: return kernels_of<MfmaDecode<T, D, 1, A>>();
-        case 2: return kernels_of<MfmaDecode<T, D, 2, A>>();
-        case 4: return kernels_of<MfmaDecode<T, D, 4, A>>();
-        case 7: return kernels_of<MfmaDecode<T, D, 7, A>>();
-        case 8: return kernels_of<MfmaDecode<T, D, 8, A>>();
-        case 16: return kernels_of<MfmaDecode<T, D, 16, A>>();
-    }
-    return Kernels();
-}
-
-// fp16 / bf16 pools: the MFMA body (decode_mfma.h).
-template <typename T, bool A>
-Kernels pick_mfma16(int D, int G) {
-    if (D == 64) return pick_mfma16_g<T, 64, A>(G);
-    if (D == 128) return pick_mfma16_g<T, 128, A>(G);
-    return Kernels();
-}
-
-template <int D, bool A>
-Kernels pick_mfma_f32_g(int G) {
-    switch (G) {
-        case 1: return kernels_of<MfmaDecode<float, D, 1, A>>();
-        case 2: return kernels_of<MfmaDecode<float, D, 2, A>>();
-        case 4: return kernels_of<MfmaDecode<float, D, 4, A>>();
-        case 7: return kernels_of<MfmaDecode<float, D, 7, A>>();
-        case 8: return kernels_of<MfmaDecode<float, D, 8, A>>();
-        case 16: return kernels_of<MfmaDecode<float, D, 16, A>>();
-    }
-    return Kernels();
-}
-
-// fp32 pools: the MFMA body (decode_mfma.h).
-template <bool A>
-Kernels pick_f32(int D, int G) {
-    if (D == 64) return pick_mfma_f32_g<64, A>(G);
-    if (D == 128) return pick_mfma_f32_g<128, A>(G);
-    return Kernels();
-}
-
-// The tuned kernels of a pool type, plain or fused-append.
-template <bool A>
-Kernels pick_tuned(int dtype, int D, int G) {
-    if (dtype == LLKV_DTYPE_F32) return pick_f32<A>(D, G);
-    if (dtype == LLKV_DTYPE_F16) return pick_mfma16<_Float16, A>(D, G);
-    if (dtype == LLKV_DTYPE_BF16) return pick_mfma16<bf16_t, A>(D, G);
+// The tuned kernels of a pool type, plain or fused-append (decode_tuned_*.hip).
+Kernels pick_tuned(int dtype, int D, int G, bool append) {
+    if (dtype == LLKV_DTYPE_F32) return tuned_kernels_f32(D, G, append);
+    if (dtype == LLKV_DTYPE_F16) return tuned_kernels_f16(D, G, append);
+    if (dtype == LLKV_DTYPE_BF16) return tuned_kernels_bf16(D, G, append);
     return Kernels();
 }
 
@@ -580,7 +435,7 @@ int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_ne
                          ((size_t)num_kv_heads * head_dim * es) % 16 == 0;
     Kernels ks;
     if (block_size == kPage && aligned) {
-        ks = k_new ? pick_tuned<true>(dtype, head_dim, G) : pick_tuned<false>(dtype, head_dim, G);
+        ks = pick_tuned(dtype, head_dim, G, k_new != nullptr);
     }
     const int max_pages_hint = (max_seq_len + block_size - 1) / block_size;
     bool balanced = false;

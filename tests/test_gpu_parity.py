@@ -217,6 +217,8 @@ FUSED = [
     ("bf16_S4", 40, 14, 2, 64, torch.bfloat16, 4, (1, 700)),
     ("f16_G16_S16", 8, 16, 1, 64, torch.float16, 16, (500, 5000)),
     ("f32_generic_D67", 12, 4, 2, 67, torch.float32, 0, (1, 300)),
+    ("f16_G6_D128_auto", 48, 12, 2, 128, torch.float16, 0, (1, 3000)),
+    ("f32_G5_S3", 20, 10, 2, 64, torch.float32, 3, (1, 900)),
 ]
 
 
@@ -396,7 +398,14 @@ EDGE = [
     ("gqa_8_2", 8, 2, 64, [200, 33], torch.float32),
     ("mqa_hkv1", 8, 1, 64, [200, 33], torch.float32),
     ("mha", 4, 4, 64, [200, 33], torch.float32),
-    ("gqa_g3_generic", 6, 2, 64, [130, 5], torch.float32),
+    ("gqa_g3", 6, 2, 64, [130, 5], torch.float32),
+    # group sizes 3, 5, 6 (Llama-3.2-3B, Qwen2.5-14B/32B, Qwen2.5-1.5B head layouts)
+    ("fp16_D128_g3", 24, 8, 128, [1, 333, 1600], torch.float16),
+    ("fp16_D128_g5", 40, 8, 128, [16, 17, 1200], torch.float16),
+    ("fp32_D128_g6", 12, 2, 128, [5, 640, 1500], torch.float32),
+    ("bf16_D64_g6", 12, 2, 64, [31, 900], torch.bfloat16),
+    ("fp32_D64_g5", 10, 2, 64, [64, 1029], torch.float32),
+    ("gqa_g12_generic", 12, 1, 64, [130, 5], torch.float32),
     ("fp16_D128_g4", 32, 8, 128, [1, 500, 2049], torch.float16),
     ("fp16_D64_g7", 14, 2, 64, [7, 700], torch.float16),
     ("bf16_D64_g7", 14, 2, 64, [7, 700], torch.bfloat16),
