@@ -33,6 +33,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import statistics
@@ -256,7 +257,30 @@ def bench_other_configs(torch, kc, wl):
                         "prefill_us": round(pre_us, 1),
                         "prefill_mfma_frac": round(pf / (pre_us * 1e-6) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4)}
     res["rope_append_cfg5_step"] = bench_rope_append(torch, kc, dec, pre, kp, vp, dsl_slots, pslots)
+    del kp, vp
+    res["first_prefill_fp32_8x512"] = bench_first_prefill(torch, kc)
     return res
+
+
+def bench_first_prefill(torch, kc):
+    """Batched first prefill as EngineServer::step issues it (fp32, contiguous K/V): 8 entries
+    of 512 tokens, Qwen2.5-0.5B heads (14/2/64), causal within each entry."""
+    import numpy as np
+    dev = torch.device("cuda:0")
+    hq, hkv, d, ntok = 14, 2, 64, [512] * 8
+    n = len(ntok)
+    cum = np.concatenate([[0], np.cumsum(ntok)]).astype(np.int32)
+    ptot = int(cum[-1])
+    g = torch.Generator(device="cpu").manual_seed(8)
+    q, k, v = (torch.randn(ptot, h, d, generator=g).to(dev) for h in (hq, hkv, hkv))
+    out = torch.empty_like(q)
+    t32 = lambda a: torch.as_tensor(a, dtype=torch.int32).to(dev)
+    args = (out, q, k, v, hq, hkv, d, t32(cum[:-1] * hq * d), t32(cum[:-1] * hkv * d), t32(ntok),
+            t32(cum), t32(np.zeros(n)), n, ptot, 1.0 / math.sqrt(d))
+    us = _graph_us(torch, lambda i: kc.first_prefill_attn_batched(*args, max_tokens=max(ntok)), 10)
+    flops = sum(p * (p + 1) / 2 for p in ntok) * 4 * d * hq
+    tf = flops / (us * 1e-6) / 1e12
+    return {"us": round(us, 1), "TFLOPs": round(tf, 1), "mfma_frac_of_fp32_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
 
 
 def rope_append_bytes(T, hq, hkv, d, rot, esize):

@@ -235,8 +235,13 @@ int llkv_paged_prefill(void* out, const void* q, const void* k_pool,
  * (include/lightllm/kv_cache/paged_attention.h:130-145,
  * src/kv_cache/paged_attention.cu:1230-1383): causal attention of first
  * prefill chunks over contiguous (un-paged) K/V.  Offsets are element
- * offsets, as in the reference.  max_tokens is a host upper bound of
- * num_tokens[e].  Unlike the reference this does not synchronise. */
+ * offsets, as in the reference, of row starts (multiples of Hq*D and
+ * Hkv*D, as EngineServer::step builds them, engine_server.cpp:1635-1636).
+ * max_tokens is a host upper bound of num_tokens[e] (0: P_total; a tight
+ * bound avoids launching empty query blocks).  fp32 / fp16 / bf16 with
+ * head_dim 64 or 128 and 16-byte aligned buffers run on the MFMA prefill
+ * kernels; other shapes on a row kernel.  Unlike the reference this does not
+ * synchronise. */
 int llkv_first_prefill_batched(void* out, const void* q, const void* k,
                                const void* v, int num_q_heads,
                                int num_kv_heads, int head_dim,

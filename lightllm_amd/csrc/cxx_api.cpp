@@ -201,9 +201,20 @@ void first_prefill_attn_batched_gpu_dispatch(DType dtype, void* out_ptr, const v
                                              const int* token_cumsum, const int* start_poss,
                                              int N, int P_total, float scale) {
     if (D > 256) throw std::runtime_error("first_prefill_attn_batched: head_dim too large");
+    // The longest entry bounds the query blocks of the launch (P_total would
+    // launch mostly empty work-groups): one small device-to-host read, in a
+    // call that synchronises anyway.
+    int max_tokens = 0;
+    if (N > 0 && num_tokens != nullptr) {
+        std::vector<int> nt(N);
+        hip_throw(hipMemcpy(nt.data(), num_tokens, N * sizeof(int), hipMemcpyDeviceToHost),
+                  "first_prefill_attn_batched");
+        max_tokens = *std::max_element(nt.begin(), nt.end());
+        if (max_tokens <= 0) max_tokens = P_total;
+    }
     throw_if(llkv_first_prefill_batched(out_ptr, q_ptr, k_ptr, v_ptr, Hq, Hkv, D, offsets, kv_offsets,
-                                        num_tokens, token_cumsum, start_poss, N, P_total, 0, scale,
-                                        static_cast<int>(dtype), nullptr),
+                                        num_tokens, token_cumsum, start_poss, N, P_total, max_tokens,
+                                        scale, static_cast<int>(dtype), nullptr),
              "first_prefill_attn_batched");
     // The reference synchronises the device after this launch (:1349, :1382).
     hip_throw(hipDeviceSynchronize(), "first_prefill_attn_batched");

@@ -190,7 +190,7 @@ extern "C" int llkv_paged_prefill(void* out, const void* q, const void* k_pool,
         return set_error(LLKV_ERR_INVALID, "%s: null pointer", fn);
     hipStream_t st = (hipStream_t)stream;
 
-    MfmaPrefillArgs m;
+    MfmaPrefillArgs m = {};
     m.out = out;
     m.q = q;
     m.k = k_pool;
@@ -235,7 +235,6 @@ extern "C" int llkv_first_prefill_batched(void* out, const void* q, const void* 
                                           int N, int P_total, int max_tokens, float scale,
                                           int dtype, void* stream) {
     (void)start_poss;   // causal test start+pos <= start+local reduces to pos <= local
-    (void)max_tokens;
     const char* fn = "llkv_first_prefill_batched";
     if (N == 0 || P_total == 0) return LLKV_OK;
     if (N < 0 || P_total < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0)
@@ -247,6 +246,26 @@ extern "C" int llkv_first_prefill_batched(void* out, const void* q, const void* 
     if (dtype_bytes(dtype) == 0) return set_error(LLKV_ERR_INVALID, "%s: unsupported dtype %d", fn, dtype);
     if (!out || !q || !k || !v || !offsets || !kv_offsets || !num_tokens || !token_cumsum)
         return set_error(LLKV_ERR_INVALID, "%s: null pointer", fn);
+    const int bound = (max_tokens > 0 && max_tokens < P_total) ? max_tokens : P_total;
+    MfmaPrefillArgs m = {};
+    m.out = out;
+    m.q = q;
+    m.k = k;
+    m.v = v;
+    m.N = N;
+    m.Hq = num_q_heads;
+    m.Hkv = num_kv_heads;
+    m.causal = 1;
+    m.scale_log2 = scale * kLog2e;
+    m.contig = 1;
+    m.q_off = offsets;
+    m.kv_off = kv_offsets;
+    m.ntok = num_tokens;
+    m.q_row = num_q_heads * head_dim;
+    const int r = launch_prefill_mfma(m, head_dim, kPage, dtype, P_total, bound, bound, nullptr, 0,
+                                      (hipStream_t)stream);
+    if (r != -1) return r;   // -1: shape not covered by the MFMA kernels
+
     RowArgs a = {};
     a.out = out;
     a.q = q;

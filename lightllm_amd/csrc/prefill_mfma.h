@@ -41,6 +41,14 @@ struct MfmaPrefillArgs {
     const int* cu_q;
     const int* lens;
     int max_blocks, N, Hq, Hkv, causal;
+    // contiguous K/V (first prefill): sequence n's q rows start at element
+    // q_off[n] (a multiple of q_row = Hq * D), its num_tokens ntok[n] keys at
+    // element kv_off[n] of k / v; cu_q, lens and bt are unused.
+    int contig;
+    const int* q_off;
+    const int* kv_off;
+    const int* ntok;
+    int q_row;
     float scale_log2;
     int qblocks;      // query blocks per sequence
     int max_chunks;   // key chunks per (sequence, query block)
@@ -55,7 +63,8 @@ size_t prefill_mfma_workspace(int N, int Hq, int head_dim, int block_size, int d
                               int total_q, int max_q_len, int max_seq_len);
 
 // Returns -1 when the shape is not handled (caller falls back), else a status.
-// workspace may be NULL (then no key range is split).
+// workspace may be NULL (then no key range is split).  a.contig selects the
+// contiguous-K/V form (max_q_len = max_seq_len = the token-count bound).
 int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dtype,
                         int total_q, int max_q_len, int max_seq_len, void* workspace,
                         size_t workspace_bytes, hipStream_t st);

@@ -47,18 +47,34 @@ constexpr int BN = 64;    // keys per tile (four pages)
 // key tiles (the causal extent of the rows).  Query blocks are numbered from
 // the last, so that in a sequence the longest unit comes first.
 struct UnitInfo {
-    int q0, P, L, tiles;
+    int q0, P, L, kvo, tiles;
 };
+
+// Sequence n's first q row, new tokens P, keys L, and (contiguous K/V) the
+// element offset of its first K/V row.  Paged: rows cu_q[n] .. cu_q[n+1],
+// L = seq_lens[n] capped at the table's extent.  Contiguous (first prefill):
+// q rows from offsets[n] (a row start), P = L = num_tokens[n].
+__device__ inline void seq_geom(const MfmaPrefillArgs& a, int n, int& q0, int& P, int& L, int& kvo) {
+    if (a.contig) {
+        q0 = a.q_off[n] / a.q_row;
+        P = max(a.ntok[n], 0);
+        L = P;
+        kvo = a.kv_off[n];
+    } else {
+        q0 = a.cu_q[n];
+        P = a.cu_q[n + 1] - q0;
+        const int l = a.lens[n];
+        const int cap = a.max_blocks * kPage;
+        L = l < 0 ? 0 : (l > cap ? cap : l);
+        kvo = 0;
+    }
+}
 
 __device__ inline UnitInfo unit_info(const MfmaPrefillArgs& a, int u) {
     const int n = u / a.qblocks;
     const int qb = a.qblocks - 1 - (u % a.qblocks);
     UnitInfo r;
-    r.q0 = a.cu_q[n];
-    r.P = a.cu_q[n + 1] - r.q0;
-    int L = a.lens[n];
-    const int cap = a.max_blocks * kPage;
-    r.L = L < 0 ? 0 : (L > cap ? cap : L);
+    seq_geom(a, n, r.q0, r.P, r.L, r.kvo);
     const int q_lo = qb * BQ;
     if (q_lo >= r.P) {
         r.tiles = 0;
@@ -89,12 +105,14 @@ __device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* orde
     int* q0s = order + 2 * kRankUnits;
     int* ps = order + 3 * kRankUnits;
     int* ls = order + 4 * kRankUnits;
+    int* kvos = order + 5 * kRankUnits;
     for (int u = threadIdx.x; u < U; u += blockDim.x) {
         const UnitInfo r = unit_info(a, u);
         tiles[u] = r.tiles;
         q0s[u] = r.q0;
         ps[u] = r.P;
         ls[u] = r.L;
+        kvos[u] = r.kvo;
     }
     __syncthreads();
     for (int u = threadIdx.x; u < U; u += blockDim.x) {
@@ -108,6 +126,7 @@ __device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* orde
     info.q0 = q0s[u];
     info.P = ps[u];
     info.L = ls[u];
+    info.kvo = kvos[u];
     info.tiles = tiles[u];
     return u;
 }
@@ -134,7 +153,7 @@ constexpr int kXcds = 8;   // XCDs of an MI355X; work-groups go to them round-ro
 // j (slot-major) goes to XCD j % 8 with its G heads as that XCD's next G
 // work-groups: they run together and share their K/V reads in one L2.
 struct Work {
-    int hq, kvh, unit, n, ci, q0, P, q_lo, L, kend, t_begin, t_end;
+    int hq, kvh, unit, n, ci, q0, P, q_lo, L, kvo, kend, t_begin, t_end;
     bool direct;   // one chunk: write the output row itself
 };
 
@@ -166,6 +185,7 @@ __device__ inline bool take_work(const MfmaPrefillArgs& a, int* order, Work& wk)
     wk.q_lo = qb * BQ;
     if (wk.q_lo >= wk.P) return false;
     wk.L = ui.L;
+    wk.kvo = ui.kvo;
     int kend = a.causal ? wk.L - wk.P + min(wk.q_lo + BQ, wk.P) : wk.L;
     wk.kend = kend < 0 ? 0 : (kend > wk.L ? wk.L : kend);
     const int ntiles = (wk.kend + BN - 1) / BN;
@@ -186,12 +206,15 @@ struct Smem {
             alignas(16) uint16_t k[2][BN * KPAD];
             alignas(16) uint16_t vt[2][D * VPAD];
         };
-        int order[5 * kRankUnits];   // prologue only: unit tiles, unit at each rank, q0, P, L
+        int order[6 * kRankUnits];   // prologue only: unit tiles, unit at each rank, q0, P, L, K/V offset
     };
     int pages[kPageWindow];   // page ids [tbase, tbase + kPageWindow) of the sequence
 };
 
-template <typename T, int D>
+// CG: contiguous K/V (first prefill): key j of the sequence is row kvo + j of
+// k / v; the staged rows are clamped to the sequence's last, and there is no
+// page table.
+template <typename T, int D, bool CG>
 __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     constexpr int KPAD = Smem<D>::KPAD, VPAD = Smem<D>::VPAD;
     constexpr int KS = D / 32;            // k-steps of the QK^T product
@@ -213,8 +236,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const bool direct = wk.direct;
     const int last_page = L > 0 ? (L - 1) / kPage : 0;
     const int* bt = a.bt + (int64_t)n * a.max_blocks;
-    const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)kvh * D;
-    const T* vg = reinterpret_cast<const T*>(a.v) + (int64_t)kvh * D;
+    const T* kg = reinterpret_cast<const T*>(a.k) + (int64_t)kvh * D + (CG ? (int64_t)wk.kvo : 0);
+    const T* vg = reinterpret_cast<const T*>(a.v) + (int64_t)kvh * D + (CG ? (int64_t)wk.kvo : 0);
 
     // ---- Q^T operands (B of S^T = K Q^T), kept in registers; loaded after the
     // page ids so that their latency overlaps the first tile's ------------
@@ -265,6 +288,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     u32x4 vr[VT_T][2];
     // Per-thread byte offsets inside a page and page slot of each staged row;
     // a load is then base + phys * page_bytes + offset (one 32x32->64 multiply-add).
+    // Contiguous K/V: the key within the tile and the byte offset in the row.
     const uint32_t row_bytes = (uint32_t)(a.Hkv * D * sizeof(T));
     const uint32_t page_bytes = row_bytes * kPage;
     const char* kb = reinterpret_cast<const char*>(kg);
@@ -275,17 +299,32 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     for (int j = 0; j < KCH_T; ++j) {
         const int ch = tid + 256 * j;
         const int key = ch / (D / 8), c = ch % (D / 8);
-        kslot[j] = key >> 4;
-        koff[j] = (uint32_t)(key & 15) * row_bytes + (uint32_t)c * 16u;
+        kslot[j] = CG ? key : key >> 4;
+        koff[j] = (CG ? 0u : (uint32_t)(key & 15) * row_bytes) + (uint32_t)c * 16u;
     }
 #pragma unroll
     for (int j = 0; j < VT_T; ++j) {
         const int task = tid + 256 * j;
         const int kp = task % (BN / 2), c = task / (BN / 2);
-        vslot[j] = (2 * kp) >> 4;
-        voff[j] = (uint32_t)((2 * kp) & 15) * row_bytes + (uint32_t)c * 16u;
+        vslot[j] = CG ? 2 * kp : (2 * kp) >> 4;
+        voff[j] = (CG ? 0u : (uint32_t)((2 * kp) & 15) * row_bytes) + (uint32_t)c * 16u;
     }
     auto load_tile = [&](int t, u32x4 (&kreg)[KCH_T], u32x4 (&vreg)[VT_T][2]) {
+        if constexpr (CG) {   // rows past the sequence's last are staged as the last
+            const int key0 = t * BN, last = L - 1;
+#pragma unroll
+            for (int j = 0; j < KCH_T; ++j)
+                kreg[j] = *reinterpret_cast<const u32x4*>(
+                    kb + (uint64_t)min(key0 + kslot[j], last) * row_bytes + koff[j]);
+#pragma unroll
+            for (int j = 0; j < VT_T; ++j) {
+                vreg[j][0] = *reinterpret_cast<const u32x4*>(
+                    vb + (uint64_t)min(key0 + vslot[j], last) * row_bytes + voff[j]);
+                vreg[j][1] = *reinterpret_cast<const u32x4*>(
+                    vb + (uint64_t)min(key0 + vslot[j] + 1, last) * row_bytes + voff[j]);
+            }
+            return;
+        }
         // pages past the sequence's last are staged as the last page (valid memory)
         const int* pg = sm.pages + (4 * t - tbase);
 #pragma unroll
@@ -327,6 +366,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 
     // Page ids live in LDS so that no K/V load waits behind a table load.
     auto stage_pages = [&](int base) {
+        if constexpr (CG) return;   // no page table
         tbase = base;
         for (int i = tid; i < kPageWindow; i += 256) sm.pages[i] = bt[min(base + i, last_page)];
         lds_barrier();   // the page ids are in LDS; no global load needs to have landed
@@ -582,12 +622,12 @@ struct SmemF32 {
             alignas(16) float k[KNB][BN * KPAD];
             alignas(16) float vt[VNB][D * VPAD];
         };
-        int order[5 * kRankUnits];
+        int order[6 * kRankUnits];
     };
     int pages[kPageWindow];
 };
 
-template <int D>
+template <int D, bool CG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? LLKV_F32_WPE64 : LLKV_F32_WPE128)))
 void prefill_f32_kernel(MfmaPrefillArgs a) {
     typedef SmemF32<D> S;
@@ -645,27 +685,35 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
     u32x4 vr[VT_T][4];
     const uint32_t row_bytes = (uint32_t)(a.Hkv * D * sizeof(float));
     const uint32_t page_bytes = row_bytes * kPage;
-    const char* kb_ = reinterpret_cast<const char*>(reinterpret_cast<const float*>(a.k) + (int64_t)kvh * D);
-    const char* vb_ = reinterpret_cast<const char*>(reinterpret_cast<const float*>(a.v) + (int64_t)kvh * D);
+    const int64_t kv0 = (int64_t)kvh * D + (CG ? (int64_t)wk.kvo : 0);
+    const char* kb_ = reinterpret_cast<const char*>(reinterpret_cast<const float*>(a.k) + kv0);
+    const char* vb_ = reinterpret_cast<const char*>(reinterpret_cast<const float*>(a.v) + kv0);
     uint32_t koff[KCH_T], voff[VT_T];
     int kslot[KCH_T], vslot[VT_T];
 #pragma unroll
     for (int j = 0; j < KCH_T; ++j) {
         const int ch = tid + 256 * j;
         const int key = ch / (D / 4), c = ch % (D / 4);
-        kslot[j] = key >> 4;
-        koff[j] = (uint32_t)(key & 15) * row_bytes + (uint32_t)c * 16u;
+        kslot[j] = CG ? key : key >> 4;   // contiguous K/V: the key within the tile
+        koff[j] = (CG ? 0u : (uint32_t)(key & 15) * row_bytes) + (uint32_t)c * 16u;
     }
 #pragma unroll
     for (int j = 0; j < VT_T; ++j) {
         const int task = tid + 256 * j;
         const int kq = task % (BN / 4), c = task / (BN / 4);   // keys 4kq .. 4kq+3, dims 4c .. 4c+3
-        vslot[j] = (4 * kq) >> 4;
-        voff[j] = (uint32_t)((4 * kq) & 15) * row_bytes + (uint32_t)c * 16u;
+        vslot[j] = CG ? 4 * kq : (4 * kq) >> 4;
+        voff[j] = (CG ? 0u : (uint32_t)((4 * kq) & 15) * row_bytes) + (uint32_t)c * 16u;
     }
     // Next-tile staging in two halves (K, then V^T), so that only one half's
     // registers are live at a time.
     auto load_k = [&](int t) {
+        if constexpr (CG) {   // rows past the sequence's last are staged as the last
+#pragma unroll
+            for (int j = 0; j < KCH_T; ++j)
+                kr[j] = *reinterpret_cast<const u32x4*>(
+                    kb_ + (uint64_t)min(t * BN + kslot[j], L - 1) * row_bytes + koff[j]);
+            return;
+        }
         const int* pg = sm.pages + (4 * t - tbase);
 #pragma unroll
         for (int j = 0; j < KCH_T; ++j) {
@@ -674,6 +722,15 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
         }
     };
     auto load_v = [&](int t) {
+        if constexpr (CG) {
+#pragma unroll
+            for (int j = 0; j < VT_T; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    vr[j][r] = *reinterpret_cast<const u32x4*>(
+                        vb_ + (uint64_t)min(t * BN + vslot[j] + r, L - 1) * row_bytes + voff[j]);
+            return;
+        }
         const int* pg = sm.pages + (4 * t - tbase);
 #pragma unroll
         for (int j = 0; j < VT_T; ++j) {
@@ -703,6 +760,7 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
         }
     };
     auto stage_pages = [&](int base) {
+        if constexpr (CG) return;   // no page table
         tbase = base;
         for (int i = tid; i < kPageWindow; i += 256) sm.pages[i] = bt[min(base + i, last_page)];
         lds_barrier();
@@ -882,14 +940,11 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
     const int hq = blockIdx.x, unit = blockIdx.y;
     const int n = unit / a.qblocks;
     const int qb = a.qblocks - 1 - (unit % a.qblocks);
-    const int q0 = a.cu_q[n];
-    const int P = a.cu_q[n + 1] - q0;
+    int q0, P, L, kvo;
+    seq_geom(a, n, q0, P, L, kvo);
     const int q_lo = qb * BQ;
     const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
     if (q_lo + row >= P) return;
-    int L = a.lens[n];
-    const int cap = a.max_blocks * kPage;
-    L = L < 0 ? 0 : (L > cap ? cap : L);
     int kend = a.causal ? L - P + min(q_lo + BQ, P) : L;
     kend = kend < 0 ? 0 : (kend > L ? L : kend);
     const int ntiles = (kend + BN - 1) / BN;
@@ -947,15 +1002,25 @@ constexpr double kFill = LLKV_PREFILL_FILL;
 constexpr int kMinChunkTiles = 8;
 constexpr int kSizingSlots = 1024;
 
-const void* prefill_kernel_fn(int dtype, int head_dim) {
-    if (dtype == LLKV_DTYPE_F32)
-        return head_dim == 64 ? reinterpret_cast<const void*>(prefill_f32_kernel<64>)
-                              : reinterpret_cast<const void*>(prefill_f32_kernel<128>);
+typedef void (*PrefillFn)(MfmaPrefillArgs);
+
+template <bool CG>
+PrefillFn prefill_kernel_cg(int dtype, int head_dim) {
+    if (dtype == LLKV_DTYPE_F32) return head_dim == 64 ? prefill_f32_kernel<64, CG> : prefill_f32_kernel<128, CG>;
     if (dtype == LLKV_DTYPE_F16)
-        return head_dim == 64 ? reinterpret_cast<const void*>(prefill_mfma_kernel<_Float16, 64>)
-                              : reinterpret_cast<const void*>(prefill_mfma_kernel<_Float16, 128>);
-    return head_dim == 64 ? reinterpret_cast<const void*>(prefill_mfma_kernel<bf16_t, 64>)
-                          : reinterpret_cast<const void*>(prefill_mfma_kernel<bf16_t, 128>);
+        return head_dim == 64 ? prefill_mfma_kernel<_Float16, 64, CG> : prefill_mfma_kernel<_Float16, 128, CG>;
+    return head_dim == 64 ? prefill_mfma_kernel<bf16_t, 64, CG> : prefill_mfma_kernel<bf16_t, 128, CG>;
+}
+
+PrefillFn prefill_kernel(int dtype, int head_dim, bool contig) {
+    return contig ? prefill_kernel_cg<true>(dtype, head_dim) : prefill_kernel_cg<false>(dtype, head_dim);
+}
+
+PrefillFn merge_kernel(int dtype, int head_dim) {
+    if (dtype == LLKV_DTYPE_F32) return head_dim == 64 ? prefill_merge_kernel<float, 64> : prefill_merge_kernel<float, 128>;
+    if (dtype == LLKV_DTYPE_F16)
+        return head_dim == 64 ? prefill_merge_kernel<_Float16, 64> : prefill_merge_kernel<_Float16, 128>;
+    return head_dim == 64 ? prefill_merge_kernel<bf16_t, 64> : prefill_merge_kernel<bf16_t, 128>;
 }
 
 struct ChunkPlan {
@@ -998,7 +1063,7 @@ int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dty
                         size_t workspace_bytes, hipStream_t st) {
     if (!prefill_mfma_handles(head_dim, block_size, dtype)) return -1;
     if (((uintptr_t)a.q | (uintptr_t)a.out | (uintptr_t)a.k | (uintptr_t)a.v) & 15) return -1;
-    const int slots = resident_workgroups(prefill_kernel_fn(dtype, head_dim), 256);
+    const int slots = resident_workgroups(reinterpret_cast<const void*>(prefill_kernel(dtype, head_dim, false)), 256);
     const ChunkPlan c = chunk_plan(a.N, a.Hq, total_q, max_q_len, max_seq_len, slots);
     a.qblocks = c.qblocks;
     const size_t need = prefill_mfma_workspace(a.N, a.Hq, head_dim, block_size, dtype, total_q,
@@ -1021,33 +1086,9 @@ int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dty
     const int G = a.Hq / a.Hkv;
     dim3 grid((unsigned)(((a.groups + kXcds - 1) / kXcds) * kXcds * G));
     dim3 mgrid(a.Hq, a.N * a.qblocks);
-    const bool merge = a.max_chunks > 1;
-    if (dtype == LLKV_DTYPE_F32) {
-        if (head_dim == 64) {
-            prefill_f32_kernel<64><<<grid, 256, 0, st>>>(a);
-            if (merge) prefill_merge_kernel<float, 64><<<mgrid, 256, 0, st>>>(a);
-        } else {
-            prefill_f32_kernel<128><<<grid, 256, 0, st>>>(a);
-            if (merge) prefill_merge_kernel<float, 128><<<mgrid, 256, 0, st>>>(a);
-        }
-    } else if (dtype == LLKV_DTYPE_F16) {
-        if (head_dim == 64) {
-            prefill_mfma_kernel<_Float16, 64><<<grid, 256, 0, st>>>(a);
-            if (merge) prefill_merge_kernel<_Float16, 64><<<mgrid, 256, 0, st>>>(a);
-        } else {
-            prefill_mfma_kernel<_Float16, 128><<<grid, 256, 0, st>>>(a);
-            if (merge) prefill_merge_kernel<_Float16, 128><<<mgrid, 256, 0, st>>>(a);
-        }
-    } else {
-        if (head_dim == 64) {
-            prefill_mfma_kernel<bf16_t, 64><<<grid, 256, 0, st>>>(a);
-            if (merge) prefill_merge_kernel<bf16_t, 64><<<mgrid, 256, 0, st>>>(a);
-        } else {
-            prefill_mfma_kernel<bf16_t, 128><<<grid, 256, 0, st>>>(a);
-            if (merge) prefill_merge_kernel<bf16_t, 128><<<mgrid, 256, 0, st>>>(a);
-        }
-    }
-    return check_launch("llkv_paged_prefill");
+    prefill_kernel(dtype, head_dim, a.contig != 0)<<<grid, 256, 0, st>>>(a);
+    if (a.max_chunks > 1) merge_kernel(dtype, head_dim)<<<mgrid, 256, 0, st>>>(a);
+    return check_launch(a.contig ? "llkv_first_prefill_batched" : "llkv_paged_prefill");
 }
 
 }  // namespace llkv

@@ -370,12 +370,14 @@ def prefill_paged_attention(q: torch.Tensor, block_table: torch.Tensor, max_bloc
 def first_prefill_attn_batched(out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                hq: int, hkv: int, d: int, offsets, kv_offsets, num_tokens,
                                token_cumsum, start_poss, n: int, p_total: int, scale: float,
-                               stream=None) -> None:
-    """Reference first_prefill_attn_batched_gpu_dispatch (paged_attention.h:138-145)."""
+                               stream=None, max_tokens: int = 0) -> None:
+    """Reference first_prefill_attn_batched_gpu_dispatch (paged_attention.h:138-145).
+    offsets / kv_offsets are element offsets of row starts; max_tokens is a host upper bound
+    of num_tokens (0: p_total)."""
     for name, t in (("offsets", offsets), ("kv_offsets", kv_offsets), ("num_tokens", num_tokens),
                     ("token_cumsum", token_cumsum), ("start_poss", start_poss)):
         _require(t, torch.int32, name)
     check(lib().llkv_first_prefill_batched(_ptr(out), _ptr(q), _ptr(k), _ptr(v), hq, hkv, d,
                                            _ptr(offsets), _ptr(kv_offsets), _ptr(num_tokens),
-                                           _ptr(token_cumsum), _ptr(start_poss), n, p_total, 0,
+                                           _ptr(token_cumsum), _ptr(start_poss), n, p_total, max_tokens,
                                            scale, dtype_code(q.dtype), _stream(stream)))

@@ -50,8 +50,9 @@ def check_lowp(got: torch.Tensor, ref: np.ndarray, what: str, rtol: float):
     # relative to each output vector's RMS (over head_dim), plus the element itself
     rms = np.sqrt(np.mean(ref ** 2, axis=-1, keepdims=True))
     bound = rtol * (np.abs(ref) + rms)
+    ratio = np.divide(err, bound, out=np.where(err > 0, np.inf, 0.0), where=bound > 0)
     say(f"  {what}: max abs err {float(err.max()):.3e}, "
-        f"worst err/bound {float((err / bound).max()):.3f}")
+        f"worst err/bound {float(ratio.max()):.3f}")
     assert np.all(err <= bound), f"{what}: {int((err > bound).sum())} elements out of tolerance"
 
 
@@ -611,40 +612,57 @@ def test_prefill_loose_bounds(dtype):
     check_lowp(tight, ref, "prefill tight bounds", 2e-3 if dtype == torch.float16 else 1.6e-2)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
-def test_first_prefill_batched(dtype):
-    say(f"first prefill batched {dtype}")
-    g = torch.Generator().manual_seed(14)
-    hq, hkv, d = 14, 2, 64
-    ntok = [1, 37, 128, 300]
+FIRST = [
+    # (name, Hq, Hkv, D, num_tokens per entry, rows of gap before each entry, dtype, pass max_tokens)
+    ("fp32_small", 14, 2, 64, [1, 37, 128, 300], [0, 0, 0, 0], torch.float32, False),
+    ("fp16_small", 14, 2, 64, [1, 37, 128, 300], [0, 0, 0, 0], torch.float16, False),
+    ("fp32_gaps_D128", 32, 8, 128, [200, 5, 640], [3, 17, 1], torch.float32, True),
+    ("fp16_gaps_D128", 32, 8, 128, [200, 5, 640], [3, 17, 1], torch.float16, True),
+    ("bf16_long", 14, 2, 64, [1500, 77], [0, 9], torch.bfloat16, True),
+    ("fp32_many", 14, 2, 64, [(53 * i) % 300 + 1 for i in range(40)], [i % 3 for i in range(40)],
+     torch.float32, True),
+    ("fp32_generic_D67", 4, 2, 67, [33, 100], [0, 2], torch.float32, False),
+]
+
+
+@pytest.mark.parametrize("name,hq,hkv,d,ntok,gaps,dtype,tight", FIRST, ids=[f[0] for f in FIRST])
+def test_first_prefill_batched(name, hq, hkv, d, ntok, gaps, dtype, tight):
+    """Batched first prefill over contiguous K/V: entries at row offsets with gaps between
+    them (as EngineServer::step lays out a step's tokens), the last entry ending at the end of
+    the K/V buffers, with and without the host bound on num_tokens."""
+    say(f"first prefill batched {name}")
+    g = torch.Generator().manual_seed(14 + len(name))
     n = len(ntok)
     cum = np.concatenate([[0], np.cumsum(ntok)]).astype(np.int32)
-    offs = (cum[:-1] * hq * d).astype(np.int32)
-    kvoffs = (cum[:-1] * hkv * d).astype(np.int32)
+    starts_rows = np.cumsum(np.array(gaps) + np.concatenate([[0], ntok[:-1]])).astype(np.int32)
+    rows = int(starts_rows[-1] + ntok[-1])
+    offs = (starts_rows * hq * d).astype(np.int32)
+    kvoffs = (starts_rows * hkv * d).astype(np.int32)
     starts = np.zeros(n, dtype=np.int32)
     ptot = int(cum[-1])
-    q = torch.randn(ptot, hq, d, generator=g).to(dtype)
-    k = torch.randn(ptot, hkv, d, generator=g).to(dtype)
-    v = torch.randn(ptot, hkv, d, generator=g).to(dtype)
-    out = torch.zeros(ptot, hq, d, dtype=dtype, device=DEV)
+    q = torch.randn(rows, hq, d, generator=g).to(dtype)
+    k = torch.randn(rows, hkv, d, generator=g).to(dtype)
+    v = torch.randn(rows, hkv, d, generator=g).to(dtype)
+    out = torch.zeros(rows, hq, d, dtype=dtype, device=DEV)
     t32 = lambda a: torch.as_tensor(a, dtype=torch.int32).to(DEV)
     kc.first_prefill_attn_batched(out, q.to(DEV), k.to(DEV), v.to(DEV), hq, hkv, d, t32(offs),
                                   t32(kvoffs), t32(ntok), t32(cum), t32(starts), n, ptot,
-                                  1.0 / math.sqrt(d))
+                                  1.0 / math.sqrt(d), max_tokens=max(ntok) if tight else 0)
     torch.cuda.synchronize()
-    # reference rule: entry e is causal over its own contiguous keys
-    ref = np.zeros((ptot, hq, d))
+    # reference rule: entry e is causal over its own contiguous keys; gap rows stay untouched
+    ref = np.zeros((rows, hq, d))
     for e in range(n):
-        s, t = cum[e], cum[e + 1]
+        s, t = int(starts_rows[e]), int(starts_rows[e] + ntok[e])
         ref[s:t] = oracle.prefill_attention(q[s:t].float().numpy(), k[s:t].float().numpy(),
                                             v[s:t].float().numpy(), True, f64=True)
     if dtype == torch.float32:
-        check_fp32(out, ref, "first_prefill fp32")
-        r32 = oracle.first_prefill_batched(q.numpy(), k.numpy(), v.numpy(), hq, hkv, d, offs, kvoffs,
-                                           ntok, cum, starts, 1.0 / math.sqrt(d), ptot)
-        say(f"  (restated kernel oracle vs double: {np.abs(r32 - ref).max():.3e})")
+        check_fp32(out, ref, name)
+        if not any(gaps):
+            r32 = oracle.first_prefill_batched(q.numpy(), k.numpy(), v.numpy(), hq, hkv, d, offs,
+                                               kvoffs, ntok, cum, starts, 1.0 / math.sqrt(d), ptot)
+            say(f"  (restated kernel oracle vs double: {np.abs(r32 - ref).max():.3e})")
     else:
-        check_lowp(out, ref, "first_prefill fp16", 2e-3)
+        check_lowp(out, ref, name, 2e-3 if dtype == torch.float16 else 1.6e-2)
 
 
 # ---------------------------------------------------------------------------
