@@ -23,8 +23,9 @@
 // When the units alone would not fill the GPU, key ranges are cut into chunks
 // of chunk_tiles tiles, one work-group each (N x qblocks x max_chunks x Hq
 // work-groups, the q heads of one kv head on one XCD), so that a cached prefix of thousands of keys does not
-// serialise on one work-group; their fp32 partials (normalised rows +
-// log2-sum-exp2) are merged by prefill_merge_kernel.  The split is chosen on
+// serialise on one work-group; their partials (normalised rows, fp16 for
+// fp16 pools and fp32 otherwise, + fp32 log2-sum-exp2) are merged by
+// prefill_merge_kernel.  The split is chosen on
 // the host from the shape bounds and the kernel's resident work-group count.
 #pragma once
 
@@ -54,7 +55,7 @@ struct MfmaPrefillArgs {
     int max_chunks;   // key chunks per (sequence, query block)
     int chunk_tiles;  // key tiles per chunk
     int groups;       // N * qblocks * max_chunks * Hkv (chunk slot, kv head) work items
-    float* part_o;    // [N*qblocks*max_chunks*Hq][BQ][D] (max_chunks > 1)
+    float* part_o;    // [N*qblocks*max_chunks*Hq][BQ][D] (max_chunks > 1), fp16 elements for fp16 pools
     float* part_lse;  // [N*qblocks*max_chunks*Hq][BQ]
 };
 
