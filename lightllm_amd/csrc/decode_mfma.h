@@ -98,7 +98,12 @@ template <typename T16, int D> struct ScoreOps16 {
 #pragma unroll
         for (int ks = 0; ks < NK; ++ks) k[ks] = *reinterpret_cast<const mu32x4*>(krow + 32 * ks + 8 * g);
     }
-    __device__ static mf32x4 mma(const mu32x4& a, const mu32x4& b, mf32x4 c);
+    __device__ static mf32x4 mma(const mu32x4& a, const mu32x4& b, mf32x4 c) {
+        if constexpr (Elem<T16>::kDtype == LLKV_DTYPE_F16)
+            return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf16x8, a), __builtin_bit_cast(mf16x8, b), c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mbf16x8, a), __builtin_bit_cast(mbf16x8, b), c, 0, 0, 0);
+    }
     __device__ static mf32x4 scores(const KReg (&k)[NK], const QReg (&q)[NQ], float scale) {
         mf32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -119,22 +124,6 @@ template <typename T16, int D> struct ScoreOps16 {
     }
 };
 
-template <>
-__device__ inline mf32x4 ScoreOps16<_Float16, 64>::mma(const mu32x4& a, const mu32x4& b, mf32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf16x8, a), __builtin_bit_cast(mf16x8, b), c, 0, 0, 0);
-}
-template <>
-__device__ inline mf32x4 ScoreOps16<_Float16, 128>::mma(const mu32x4& a, const mu32x4& b, mf32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf16x8, a), __builtin_bit_cast(mf16x8, b), c, 0, 0, 0);
-}
-template <>
-__device__ inline mf32x4 ScoreOps16<bf16_t, 64>::mma(const mu32x4& a, const mu32x4& b, mf32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mbf16x8, a), __builtin_bit_cast(mbf16x8, b), c, 0, 0, 0);
-}
-template <>
-__device__ inline mf32x4 ScoreOps16<bf16_t, 128>::mma(const mu32x4& a, const mu32x4& b, mf32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mbf16x8, a), __builtin_bit_cast(mbf16x8, b), c, 0, 0, 0);
-}
 template <int D> struct ScoreOps<_Float16, D> : ScoreOps16<_Float16, D> {};
 template <int D> struct ScoreOps<bf16_t, D> : ScoreOps16<bf16_t, D> {};
 
@@ -154,7 +143,8 @@ struct MfmaDecode {
     static constexpr int GQ = G, HD = D;
     // Resident waves per SIMD the register budget is held to: 5 (<= 96
     // registers) for head_dim 64; head_dim 128 needs more and gets 4.
-    static constexpr int kWavesPerEU = D == 64 ? 5 : 4;
+    // head_dim 256 needs ~2x the registers of 128 (16-bit pools still spill ~25).
+    static constexpr int kWavesPerEU = D == 64 ? 5 : (D == 128 ? 4 : 2);
     // Segments per round: two where the LDS for the parked states stays small.
     static constexpr int kSegMax = G * D <= 512 ? 2 : 1;
 

@@ -220,6 +220,7 @@ FUSED = [
     ("f32_generic_D67", 12, 4, 2, 67, torch.float32, 0, (1, 300)),
     ("f16_G6_D128_auto", 48, 12, 2, 128, torch.float16, 0, (1, 3000)),
     ("f32_G5_S3", 20, 10, 2, 64, torch.float32, 3, (1, 900)),
+    ("f16_D256_G2_auto", 24, 16, 8, 256, torch.float16, 0, (1, 2500)),
 ]
 
 
@@ -396,6 +397,10 @@ EDGE = [
     ("D32", 4, 2, 32, [40, 100], torch.float32),
     ("D128_hq32_hkv8", 32, 8, 128, [300, 17], torch.float32),
     ("D256", 8, 2, 256, [77, 300], torch.float32),
+    # head_dim 256 on the MFMA body (Gemma-2 / Gemma-3 head layouts: G = 2)
+    ("fp16_D256_g2", 16, 8, 256, [1, 129, 1500], torch.float16),
+    ("bf16_D256_g8", 8, 1, 256, [40, 700], torch.bfloat16),
+    ("fp32_D256_g1", 4, 4, 256, [17, 333], torch.float32),
     ("gqa_8_2", 8, 2, 64, [200, 33], torch.float32),
     ("mqa_hkv1", 8, 1, 64, [200, 33], torch.float32),
     ("mha", 4, 4, 64, [200, 33], torch.float32),
