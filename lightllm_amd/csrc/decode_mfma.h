@@ -41,6 +41,11 @@ typedef float mf32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int mu32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int mu32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 mf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mf16x4 __attribute__((ext_vector_type(4)));
+
+#ifndef LLKV_DECODE_HALF_PV
+#define LLKV_DECODE_HALF_PV 1
+#endif
 typedef __bf16 mbf16x8 __attribute__((ext_vector_type(8)));
 
 // Score operands S^T = K Q^T per element type.  load_q fills the Q^T operand
@@ -141,6 +146,12 @@ struct MfmaDecode {
     static constexpr int VH = D / 64;         // 16-byte V vectors per lane per token
     static constexpr int MD = (D + 63) / 64;
     static constexpr int GQ = G, HD = D;
+    // fp16 pools at head_dim 256: O^T = V^T P^T on v_mfma_f32_16x16x16_f16
+    // (P rounded to fp16, as in the prefill): 127.8 -> 113.1 us on a B = 64
+    // Gemma-2 shape.  At head_dim 64 / 128 the page loop is not bound by its
+    // MFMAs and this form measured 1-2 % slower, so those, and fp32 / bf16
+    // pools, keep v_mfma_f32_16x16x4f32 with V widened and P in fp32.
+    static constexpr bool kHalfPV = LLKV_DECODE_HALF_PV && Elem<T>::kDtype == LLKV_DTYPE_F16 && D == 256;
     // Resident waves per SIMD the register budget is held to: 5 (<= 96
     // registers) for head_dim 64; head_dim 128 needs more and gets 4.
     // head_dim 256 needs ~2x the registers of 128 (16-bit pools still spill ~25).
@@ -214,7 +225,8 @@ struct MfmaDecode {
         };
 
         typename Ops::KReg kr[Ops::NK];
-        float4 vr[VH][4];
+        float4 vr[VH][4];    // fp32 V (fp32 / bf16 pools)
+        mu32x2 vh[VH][4];    // raw fp16 V (fp16 pools)
         for (int k = 0;; ++k) {
             const int j = w + W * k;
             if (j >= np_total) break;
@@ -263,7 +275,10 @@ struct MfmaDecode {
                               (phys * kPage + 4 * g + i) * row_elems + 4 * c;
                 if (newpage && 4 * g + i == snew_r) vp = reinterpret_cast<const T*>(a.vnew) + nrow + 4 * c;
 #pragma unroll
-                for (int h = 0; h < VH; ++h) vr[h][i] = Ops::load_v4(vp + 64 * h);
+                for (int h = 0; h < VH; ++h) {
+                    if constexpr (kHalfPV) vh[h][i] = *reinterpret_cast<const mu32x2*>(vp + 64 * h);
+                    else vr[h][i] = Ops::load_v4(vp + 64 * h);
+                }
             }
             // The fused variant's pointer selects make the scheduler sink the V
             // loads next to their MFMAs; keep all of the page's loads first.
@@ -293,6 +308,24 @@ struct MfmaDecode {
             lsum = fmaf(lsum, corr, ps);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+            if constexpr (kHalfPV) {
+                // One v_mfma_f32_16x16x16_f16 per output tile: the lane's 4x4
+                // block (tokens 4g + i, dims 4c + j) gives tile (h, j) its A
+                // operand (tokens 4g .. 4g + 3 of dim 64h + 4c + j) with two
+                // v_perm_b32, and its own scores p[0..3] are the B operand.
+                const mu32x2 pb = {pack_h2(p[0], p[1]), pack_h2(p[2], p[3])};
+#pragma unroll
+                for (int h = 0; h < VH; ++h)
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const unsigned sel = (jj & 1) ? 0x07060302u : 0x05040100u;
+                        const int wd = jj >> 1;
+                        const mu32x2 av = {__builtin_amdgcn_perm(vh[h][1][wd], vh[h][0][wd], sel),
+                                           __builtin_amdgcn_perm(vh[h][3][wd], vh[h][2][wd], sel)};
+                        o[4 * h + jj] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                            __builtin_bit_cast(mf16x4, av), __builtin_bit_cast(mf16x4, pb), o[4 * h + jj], 0, 0, 0);
+                    }
+            } else
 #pragma unroll
             for (int h = 0; h < VH; ++h)
 #pragma unroll
