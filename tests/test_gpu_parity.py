@@ -671,6 +671,51 @@ def test_first_prefill_batched(name, hq, hkv, d, ntok, gaps, dtype, tight):
 
 
 # ---------------------------------------------------------------------------
+# seeded random shapes over the tuned and generic paths
+# ---------------------------------------------------------------------------
+
+def _check(out, ref, dtype, what):
+    if dtype == torch.float32:
+        check_fp32(out, ref, what)
+    else:
+        check_lowp(out, ref, what, 2e-3 if dtype == torch.float16 else 1.6e-2)
+
+
+@pytest.mark.parametrize("seed", list(range(16)))
+def test_random_shapes(seed):
+    """Decode and prefill on seeded random shapes: group sizes 1-8, head_dim 64 / 128 / 256
+    (decode) and 64 / 128 (prefill), 1-4 kv heads, ragged and empty lengths, fixed and
+    automatic splits, causal and not, all three pool types."""
+    rng = np.random.default_rng(1000 + seed)
+    dtype = [torch.float32, torch.float16, torch.bfloat16][seed % 3]
+    d = int(rng.choice([64, 128, 256]))
+    g = int(rng.integers(1, 9))
+    hkv = int(rng.choice([1, 2, 4]))
+    B = int(rng.integers(1, 25))
+    lengths = [int(x) for x in rng.integers(0, 700, B)]
+    S = [0, 3][seed % 2]
+    say(f"random {seed}: decode {dtype} D={d} G={g} Hkv={hkv} B={B} S={S}")
+    need = sum((L + 1 + 15) // 16 for L in lengths)
+    case = wl.decode_case(f"rnd{seed}", B, g * hkv, hkv, d, lengths, need + 8, dtype, seed=seed)
+    out, kp, vp = run_decode(case, num_splits=S)
+    _check(out, oracle_decode(case, np_pool(kp), np_pool(vp), threads=16), dtype, f"random decode {seed}")
+
+    d = int(rng.choice([64, 128]))
+    hkv = int(rng.choice([1, 2]))
+    n = int(rng.integers(1, 5))
+    prefixes = [int(x) for x in rng.integers(0, 500, n)]
+    chunks = [int(x) for x in rng.integers(1, 200, n)]
+    causal = seed % 4 != 3
+    say(f"random {seed}: prefill {dtype} D={d} G={g} Hkv={hkv} prefixes={prefixes} chunks={chunks} "
+        f"causal={causal}")
+    nb = sum((p_ + c_ + 15) // 16 for p_, c_ in zip(prefixes, chunks)) + 4
+    pc = wl.prefill_case(f"rndp{seed}", g * hkv, hkv, d, prefixes, chunks, {}, nb, dtype, seed=seed,
+                         causal=causal)
+    out, kp, vp = run_prefill(pc)
+    _check(out, oracle_prefill(pc, kp, vp), dtype, f"random prefill {seed}")
+
+
+# ---------------------------------------------------------------------------
 # C++ API (reference signatures) on the GPU
 # ---------------------------------------------------------------------------
 
