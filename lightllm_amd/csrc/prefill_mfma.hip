@@ -1014,7 +1014,10 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
 }
 
 bool prefill_mfma_handles(int head_dim, int block_size, int dtype) {
-    return block_size == kPage && (head_dim == 64 || head_dim == 128);
+    // head_dim 256: fp16 / bf16 only (one work-group per CU; the fp32 tiles
+    // would not fit in LDS)
+    return block_size == kPage &&
+           (head_dim == 64 || head_dim == 128 || (head_dim == 256 && dtype != LLKV_DTYPE_F32));
 }
 
 // Key-range split.  When the (sequence, query block, q head) units alone
@@ -1039,8 +1042,12 @@ template <bool CG>
 PrefillFn prefill_kernel_cg(int dtype, int head_dim) {
     if (dtype == LLKV_DTYPE_F32) return head_dim == 64 ? prefill_f32_kernel<64, CG> : prefill_f32_kernel<128, CG>;
     if (dtype == LLKV_DTYPE_F16)
-        return head_dim == 64 ? prefill_mfma_kernel<_Float16, 64, CG> : prefill_mfma_kernel<_Float16, 128, CG>;
-    return head_dim == 64 ? prefill_mfma_kernel<bf16_t, 64, CG> : prefill_mfma_kernel<bf16_t, 128, CG>;
+        return head_dim == 64    ? prefill_mfma_kernel<_Float16, 64, CG>
+               : head_dim == 128 ? prefill_mfma_kernel<_Float16, 128, CG>
+                                 : prefill_mfma_kernel<_Float16, 256, CG>;
+    return head_dim == 64    ? prefill_mfma_kernel<bf16_t, 64, CG>
+           : head_dim == 128 ? prefill_mfma_kernel<bf16_t, 128, CG>
+                             : prefill_mfma_kernel<bf16_t, 256, CG>;
 }
 
 PrefillFn prefill_kernel(int dtype, int head_dim, bool contig) {
@@ -1050,8 +1057,12 @@ PrefillFn prefill_kernel(int dtype, int head_dim, bool contig) {
 PrefillFn merge_kernel(int dtype, int head_dim) {
     if (dtype == LLKV_DTYPE_F32) return head_dim == 64 ? prefill_merge_kernel<float, 64> : prefill_merge_kernel<float, 128>;
     if (dtype == LLKV_DTYPE_F16)
-        return head_dim == 64 ? prefill_merge_kernel<_Float16, 64> : prefill_merge_kernel<_Float16, 128>;
-    return head_dim == 64 ? prefill_merge_kernel<bf16_t, 64> : prefill_merge_kernel<bf16_t, 128>;
+        return head_dim == 64    ? prefill_merge_kernel<_Float16, 64>
+               : head_dim == 128 ? prefill_merge_kernel<_Float16, 128>
+                                 : prefill_merge_kernel<_Float16, 256>;
+    return head_dim == 64    ? prefill_merge_kernel<bf16_t, 64>
+           : head_dim == 128 ? prefill_merge_kernel<bf16_t, 128>
+                             : prefill_merge_kernel<bf16_t, 256>;
 }
 
 struct ChunkPlan {
