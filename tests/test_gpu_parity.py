@@ -580,6 +580,9 @@ PREFILL = [
 # many (sequence, query block, head) units: the key ranges run unsplit
 PREFILL.append(("fp16_D64_many_units", 14, 2, 64, [(37 * i) % 700 for i in range(48)], [256] * 48,
                 torch.float16, True))
+# more than 1024 (sequence, query block) units: index order instead of the longest-first ranking
+PREFILL.append(("fp32_D64_1200_units", 4, 2, 64, [(53 * i) % 300 for i in range(600)],
+                [(29 * i) % 220 + 1 for i in range(600)], torch.float32, True))
 
 
 @pytest.mark.parametrize("name,hq,hkv,d,prefixes,chunks,dtype,causal", PREFILL,
@@ -632,6 +635,9 @@ FIRST = [
      torch.float32, True),
     ("fp32_generic_D67", 4, 2, 67, [33, 100], [0, 2], torch.float32, False),
     ("fp16_D256", 16, 8, 256, [300, 41], [0, 5], torch.float16, True),
+    # more than 1024 (entry, query block) units: index order instead of the longest-first ranking
+    ("fp16_1200_units", 4, 2, 64, [(37 * i) % 250 + 1 for i in range(600)], [0] * 600, torch.float16,
+     True),
 ]
 
 
