@@ -140,6 +140,23 @@ __device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* orde
     return u;
 }
 
+// Wave priority around the MFMA clusters (s_setprio: issue arbitration among
+// the waves of one SIMD, not a queue or stream priority).  1: the S = K Q^T
+// cluster runs at raised priority, so a wave in its matrix phase issues ahead
+// of waves in their softmax (configuration 5, head_dim 128: 210 -> 201 us;
+// neutral at head_dim 64, where it stays off); 2: the PV cluster too (no gain).
+#ifndef LLKV_PF_SETPRIO
+#define LLKV_PF_SETPRIO 1
+#endif
+#define LLKV_PF_PRIO(on, p)                                \
+    do {                                                   \
+        if (on) {                                          \
+            __builtin_amdgcn_sched_barrier(0);             \
+            __builtin_amdgcn_s_setprio(p);                 \
+            __builtin_amdgcn_sched_barrier(0);             \
+        }                                                  \
+    } while (0)
+
 #ifndef LLKV_PREFILL_INTERLEAVE
 #define LLKV_PREFILL_INTERLEAVE 1
 #endif
@@ -397,6 +414,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             load_tile(t + 1, kr, vr);
         }
         __builtin_amdgcn_sched_barrier(0);   // next tile's loads issue before this tile's MFMAs
+        LLKV_PF_PRIO(LLKV_PF_SETPRIO >= 1 && D >= 128, 1);
 
         // ---- S^T = K Q^T over the 64 keys: 4 key tiles x 2 query tiles ----
         f32x4 s[4][2];
@@ -416,6 +434,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             }
         }
 
+        LLKV_PF_PRIO(LLKV_PF_SETPRIO >= 1 && D >= 128, 0);
         // ---- mask, online softmax (per query column) ----------------------
         // Scores stay raw (unscaled) until the exponent: p = 2^(s c - m) with
         // c = scale * log2(e) > 0, so the row maximum commutes with the scaling.
@@ -489,6 +508,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         // otherwise put all VALU work first).  V^T rows of the second half are
         // read as those of the first are consumed.
         softmax_half(0);
+        LLKV_PF_PRIO(LLKV_PF_SETPRIO >= 2 && D >= 128, 1);
         {
             constexpr int kMf = 2 * DT + 2;   // MFMAs per half
             uint4 va0[DT], va1[DT];
@@ -548,6 +568,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         pv_half(1);
 #endif
 
+        LLKV_PF_PRIO(LLKV_PF_SETPRIO >= 2 && D >= 128, 0);
         if (t + 1 < t_end) store_tile(buf ^ 1, kr, vr);
         __syncthreads();
     }
