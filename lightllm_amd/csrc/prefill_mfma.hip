@@ -633,6 +633,12 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 // single (53 KB), three waves per SIMD (the compiler spills ~60 registers to
 // reach 168; still 13 % faster than two waves without spills).  head_dim 128:
 // ~300 registers, one wave per SIMD, so both tiles double-buffered (137 KB).
+// The S = K Q^T cluster at raised wave priority (as in the 16-bit kernel):
+// configuration 4's shape in fp32 360-380 -> 339-344 us; neutral at
+// head_dim 128 (one wave per SIMD).
+#ifndef LLKV_F32_SETPRIO
+#define LLKV_F32_SETPRIO 1
+#endif
 #ifndef LLKV_F32_KNB64
 #define LLKV_F32_KNB64 2
 #endif
@@ -825,6 +831,7 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
 
+        LLKV_PF_PRIO(LLKV_F32_SETPRIO, 1);
         // ---- S^T = K Q^T: key tile kt holds keys 16kt .. 16kt+15 ---------
         // The two halves of the head dims accumulate apart and are added at
         // the end: half the rounding steps in each sum, which halves the
@@ -854,6 +861,7 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) s[kt][nt] += hi[nt];
         }
+        LLKV_PF_PRIO(LLKV_F32_SETPRIO, 0);
         if (next) {
             if (KNB == 1) __syncthreads();   // every wave is done with the K buffer
             store_k(KNB == 2 ? kbuf ^ 1 : 0);
