@@ -42,6 +42,7 @@ typedef unsigned int mu32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int mu32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 mf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 mf16x4 __attribute__((ext_vector_type(4)));
+typedef short ms16x4 __attribute__((ext_vector_type(4)));
 
 #ifndef LLKV_DECODE_HALF_PV
 #define LLKV_DECODE_HALF_PV 1
@@ -146,12 +147,12 @@ struct MfmaDecode {
     static constexpr int VH = D / 64;         // 16-byte V vectors per lane per token
     static constexpr int MD = (D + 63) / 64;
     static constexpr int GQ = G, HD = D;
-    // fp16 pools at head_dim 256: O^T = V^T P^T on v_mfma_f32_16x16x16_f16
-    // (P rounded to fp16, as in the prefill): 127.8 -> 113.1 us on a B = 64
-    // Gemma-2 shape.  At head_dim 64 / 128 the page loop is not bound by its
-    // MFMAs and this form measured 1-2 % slower, so those, and fp32 / bf16
-    // pools, keep v_mfma_f32_16x16x4f32 with V widened and P in fp32.
-    static constexpr bool kHalfPV = LLKV_DECODE_HALF_PV && Elem<T>::kDtype == LLKV_DTYPE_F16 && D == 256;
+    // 16-bit pools at head_dim 256: O^T = V^T P^T on the 16x16x16 f16 / bf16
+    // MFMA (P rounded to the pool type, as in the prefill): 127.8 -> 113.1 us
+    // on a B = 64 Gemma-2 shape in fp16.  At head_dim 64 / 128 the page loop is
+    // not bound by its MFMAs and this form measured 1-2 % slower, so those, and
+    // fp32 pools, keep v_mfma_f32_16x16x4f32 with V widened and P in fp32.
+    static constexpr bool kHalfPV = LLKV_DECODE_HALF_PV && Elem<T>::kDtype != LLKV_DTYPE_F32 && D == 256;
     // Resident waves per SIMD the register budget is held to: 5 (<= 96
     // registers) for head_dim 64; head_dim 128 needs more and gets 4.
     // head_dim 256 needs ~2x the registers of 128 (16-bit pools still spill ~25).
@@ -313,7 +314,9 @@ struct MfmaDecode {
                 // block (tokens 4g + i, dims 4c + j) gives tile (h, j) its A
                 // operand (tokens 4g .. 4g + 3 of dim 64h + 4c + j) with two
                 // v_perm_b32, and its own scores p[0..3] are the B operand.
-                const mu32x2 pb = {pack_h2(p[0], p[1]), pack_h2(p[2], p[3])};
+                constexpr bool kF16 = Elem<T>::kDtype == LLKV_DTYPE_F16;
+                const mu32x2 pb = kF16 ? mu32x2{pack_h2(p[0], p[1]), pack_h2(p[2], p[3])}
+                                       : mu32x2{pack_b2(p[0], p[1]), pack_b2(p[2], p[3])};
 #pragma unroll
                 for (int h = 0; h < VH; ++h)
 #pragma unroll
@@ -322,8 +325,12 @@ struct MfmaDecode {
                         const int wd = jj >> 1;
                         const mu32x2 av = {__builtin_amdgcn_perm(vh[h][1][wd], vh[h][0][wd], sel),
                                            __builtin_amdgcn_perm(vh[h][3][wd], vh[h][2][wd], sel)};
-                        o[4 * h + jj] = __builtin_amdgcn_mfma_f32_16x16x16f16(
-                            __builtin_bit_cast(mf16x4, av), __builtin_bit_cast(mf16x4, pb), o[4 * h + jj], 0, 0, 0);
+                        if constexpr (kF16)
+                            o[4 * h + jj] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                                __builtin_bit_cast(mf16x4, av), __builtin_bit_cast(mf16x4, pb), o[4 * h + jj], 0, 0, 0);
+                        else
+                            o[4 * h + jj] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                                __builtin_bit_cast(ms16x4, av), __builtin_bit_cast(ms16x4, pb), o[4 * h + jj], 0, 0, 0);
                     }
             } else
 #pragma unroll
