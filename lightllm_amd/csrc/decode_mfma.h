@@ -155,7 +155,7 @@ struct MfmaDecode {
     static constexpr bool kHalfPV = LLKV_DECODE_HALF_PV && Elem<T>::kDtype != LLKV_DTYPE_F32 && D == 256;
     // Resident waves per SIMD the register budget is held to: 5 (<= 96
     // registers) for head_dim 64; head_dim 128 needs more and gets 4.
-    // head_dim 256 needs ~2x the registers of 128 (16-bit pools still spill ~25).
+    // head_dim 256: ~200 VGPRs (two waves per SIMD, no spills; three spill 33-49).
     static constexpr int kWavesPerEU = D == 64 ? 5 : (D == 128 ? 4 : 2);
     // Segments per round: two where the LDS for the parked states stays small.
     static constexpr int kSegMax = G * D <= 512 ? 2 : 1;
