@@ -288,6 +288,12 @@ int llkv_allocator_reset(llkv_allocator* a);
 int llkv_allocator_num_free(const llkv_allocator* a);
 int llkv_allocator_num_blocks(const llkv_allocator* a);
 int llkv_allocator_ref_count(const llkv_allocator* a, int block_id);
+/* Pages of block_size tokens (K and V) that fit a byte budget in the pool's
+ * element type; the C form of BlockAllocator::blocks_for_budget (additive:
+ * the reference engine sizes its pools as fp32, engine_server.cpp:418-422).
+ * -1 for bad arguments; capped at INT32_MAX. */
+int llkv_blocks_for_budget(uint64_t budget_bytes, int block_size,
+                           int num_kv_heads, int head_dim, int dtype);
 uint64_t llkv_allocator_token_hash(const llkv_allocator* a, int block_id);
 size_t llkv_allocator_prefix_cache_size(const llkv_allocator* a);
 void* llkv_allocator_k_storage(llkv_allocator* a);

@@ -60,6 +60,7 @@ _SIGS = {
     "llkv_allocator_create": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                       POINTER(c_void_p)]),
     "llkv_allocator_destroy": (None, [c_void_p]),
+    "llkv_blocks_for_budget": (c_int, [c_uint64, c_int, c_int, c_int, c_int]),
     "llkv_allocator_allocate": (c_int, [c_void_p, c_uint64]),
     "llkv_allocator_allocate_tokens": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_int,
                                                POINTER(c_int)]),

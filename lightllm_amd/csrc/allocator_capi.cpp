@@ -129,3 +129,10 @@ extern "C" size_t llkv_allocator_storage_bytes(const llkv_allocator* a) {
 extern "C" uint64_t llkv_hash_tokens(const int* tokens, int n) {
     return lightllm::kv_cache::HashPrefixCache::hash_tokens(tokens, n);
 }
+
+extern "C" int llkv_blocks_for_budget(uint64_t budget_bytes, int block_size, int num_kv_heads,
+                                      int head_dim, int dtype) {
+    if (block_size <= 0 || num_kv_heads <= 0 || head_dim <= 0 || dtype < 0 || dtype > 2) return -1;
+    return BlockAllocator::blocks_for_budget(budget_bytes, block_size, num_kv_heads, head_dim,
+                                             static_cast<DType>(dtype));
+}

@@ -69,6 +69,16 @@ class BlockAllocator:
         else:
             self.k_storage = self.v_storage = None
 
+    @staticmethod
+    def blocks_for_budget(budget_bytes: int, block_size: int, num_kv_heads: int, head_dim: int,
+                          kv_dtype: torch.dtype) -> int:
+        """Pages (K and V) that fit `budget_bytes` in the pool's element type."""
+        n = lib().llkv_blocks_for_budget(budget_bytes, block_size, num_kv_heads, head_dim,
+                                         dtype_code(kv_dtype))
+        if n < 0:
+            raise ValueError("blocks_for_budget: bad arguments")
+        return n
+
     def __del__(self):
         h = getattr(self, "_h", None)
         if h is not None and h.value:

@@ -104,6 +104,7 @@ def test_reference_cache_tests_pass_on_this_build(prog):
 # allocator handle through the C ABI, no device storage
 # ---------------------------------------------------------------------------
 
+import torch  # noqa: E402
 from lightllm_amd import kv_cache as kc  # noqa: E402
 
 
@@ -180,6 +181,19 @@ def test_allocator_evicts_lru_on_exhaustion():
     assert a.prefix_cache_size() == 3
     a.reset()
     assert a.num_free() == 4 and a.prefix_cache_size() == 0
+
+
+def test_blocks_for_budget():
+    """Pool sizing for a byte budget in the pool's element type (K and V pages)."""
+    f = kc.BlockAllocator.blocks_for_budget
+    # Llama-3-8B heads (8 x 128) in fp16: 64 KiB per page, 4.39 million pages in 288 GB
+    assert f(288_000_000_000, 16, 8, 128, torch.float16) == 288_000_000_000 // (16 * 8 * 128 * 2 * 2)
+    assert f(1 << 30, 16, 2, 64, torch.float32) == 2 * f(1 << 30, 16, 2, 128, torch.float32)
+    assert f(1 << 30, 16, 2, 64, torch.bfloat16) == 2 * f(1 << 30, 16, 2, 64, torch.float32)
+    assert f(0, 16, 2, 64, torch.float16) == 0
+    assert f(1 << 62, 1, 1, 1, torch.float16) == 2**31 - 1   # capped
+    with pytest.raises(ValueError):
+        f(1 << 30, 0, 2, 64, torch.float16)
 
 
 def test_hash_tokens_is_fnv1a_64():
