@@ -1,6 +1,6 @@
-// MFMA paged prefill attention for gfx950 (fp16 / bf16 here, head_dim 64 /
-// 128 / 256; fp32 pools take a 16x16x4 f32 variant of the same schedule at
-// head_dim 64 / 128; 16-token pages).  Replaces the reference's scalar prefill kernels
+// MFMA paged prefill attention for gfx950 (fp16 / bf16 here; fp32 pools take
+// a 16x16x4 f32 variant of the same schedule; head_dim 64 / 128 / 256,
+// 16-token pages).  Replaces the reference's scalar prefill kernels
 // (src/kv_cache/paged_attention.cu:641-974) for these shapes.
 //
 // Work-group: 4 waves, 128 query rows of one q_head (32 per wave), keys in

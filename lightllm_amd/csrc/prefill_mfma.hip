@@ -659,8 +659,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 #endif
 template <int D>
 struct SmemF32 {
-    static constexpr int KNB = D == 64 ? LLKV_F32_KNB64 : LLKV_F32_KNB128;
-    static constexpr int VNB = D == 64 ? LLKV_F32_VNB64 : LLKV_F32_VNB128;
+    static constexpr int KNB = D == 64 ? LLKV_F32_KNB64 : (D == 128 ? LLKV_F32_KNB128 : 1);
+    static constexpr int VNB = D == 64 ? LLKV_F32_VNB64 : (D == 128 ? LLKV_F32_VNB128 : 1);
     static constexpr int KPAD = D + 4;    // floats per K row (pad: 16-byte reads of 16 rows hit distinct banks)
     static constexpr int VPAD = BN + 4;   // floats per V^T row
     union {
@@ -1043,10 +1043,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
 }
 
 bool prefill_mfma_handles(int head_dim, int block_size, int dtype) {
-    // head_dim 256: fp16 / bf16 only (one work-group per CU; the fp32 tiles
-    // would not fit in LDS)
-    return block_size == kPage &&
-           (head_dim == 64 || head_dim == 128 || (head_dim == 256 && dtype != LLKV_DTYPE_F32));
+    // head_dim 256: one work-group per CU (fp32: single-buffered tiles, 134 KB)
+    return block_size == kPage && (head_dim == 64 || head_dim == 128 || head_dim == 256);
 }
 
 // Key-range split.  When the (sequence, query block, q head) units alone
@@ -1069,7 +1067,10 @@ typedef void (*PrefillFn)(MfmaPrefillArgs);
 
 template <bool CG>
 PrefillFn prefill_kernel_cg(int dtype, int head_dim) {
-    if (dtype == LLKV_DTYPE_F32) return head_dim == 64 ? prefill_f32_kernel<64, CG> : prefill_f32_kernel<128, CG>;
+    if (dtype == LLKV_DTYPE_F32)
+        return head_dim == 64    ? prefill_f32_kernel<64, CG>
+               : head_dim == 128 ? prefill_f32_kernel<128, CG>
+                                 : prefill_f32_kernel<256, CG>;
     if (dtype == LLKV_DTYPE_F16)
         return head_dim == 64    ? prefill_mfma_kernel<_Float16, 64, CG>
                : head_dim == 128 ? prefill_mfma_kernel<_Float16, 128, CG>
@@ -1084,7 +1085,10 @@ PrefillFn prefill_kernel(int dtype, int head_dim, bool contig) {
 }
 
 PrefillFn merge_kernel(int dtype, int head_dim) {
-    if (dtype == LLKV_DTYPE_F32) return head_dim == 64 ? prefill_merge_kernel<float, 64> : prefill_merge_kernel<float, 128>;
+    if (dtype == LLKV_DTYPE_F32)
+        return head_dim == 64    ? prefill_merge_kernel<float, 64>
+               : head_dim == 128 ? prefill_merge_kernel<float, 128>
+                                 : prefill_merge_kernel<float, 256>;
     if (dtype == LLKV_DTYPE_F16)
         return head_dim == 64    ? prefill_merge_kernel<_Float16, 64>
                : head_dim == 128 ? prefill_merge_kernel<_Float16, 128>

@@ -570,10 +570,11 @@ PREFILL = [
     ("fp32_mha", 4, 4, 64, [31], [97], torch.float32, True),
     ("fp32_D64_long", 14, 2, 64, [2500, 0], [300, 40], torch.float32, True),
     ("fp32_D128_long", 32, 8, 128, [2100], [130], torch.float32, True),
-    # head_dim 256 (Gemma-2 / Gemma-3 heads): fp16 / bf16 on the MFMA kernel, fp32 on the row kernel
+    # head_dim 256 (Gemma-2 / Gemma-3 heads) on the MFMA kernels
     ("fp16_D256", 16, 8, 256, [0, 300], [200, 77], torch.float16, True),
     ("bf16_D256_long_noncausal", 8, 4, 256, [2200], [90], torch.bfloat16, False),
-    ("fp32_D256_generic", 4, 2, 256, [40], [33], torch.float32, True),
+    ("fp32_D256", 4, 2, 256, [40, 900], [33, 150], torch.float32, True),
+    ("fp32_D256_long", 8, 4, 256, [2300], [70], torch.float32, True),
 ]
 
 
