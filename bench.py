@@ -259,6 +259,35 @@ def bench_other_configs(torch, kc, wl):
     res["rope_append_cfg5_step"] = bench_rope_append(torch, kc, dec, pre, kp, vp, dsl_slots, pslots)
     del kp, vp
     res["first_prefill_fp32_8x512"] = bench_first_prefill(torch, kc)
+    res.update(bench_head_dim_256(torch, kc, wl))
+    return res
+
+
+def bench_head_dim_256(torch, kc, wl):
+    """Gemma-2 head layout (16 q / 8 kv heads, head_dim 256), fp16: decode of 64 sequences with
+    contexts U[128, 2048] and prefill of 4 x 512 tokens on prefixes {0, 1024, 2048, 512}."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(128, 2049, (64,), generator=g).tolist()
+    need = sum((L + 1 + 15) // 16 for L in lens)
+    c = wl.decode_case("gemma2_decode", 64, 16, 8, 256, lens, need + 8, torch.float16, seed=3)
+    kp, vp = c.k_pool.to(dev), c.v_pool.to(dev)
+    q, bt, sl = c.q.to(dev), c.block_table.to(dev), c.seq_lens.to(dev)
+    out = torch.empty_like(q)
+    us = _graph_us(torch, lambda i: kc.paged_decode(q, kp, vp, bt, sl, c.max_seq_len, out=out), 20)
+    res = {"head_dim256_decode_fp16_B64": {"us": round(us, 1),
+                                           "GBps": round(wl.decode_bytes(c) / (us * 1e-6) / 1e9, 1)}}
+    del kp, vp
+    p = wl.prefill_case("gemma2_prefill", 16, 8, 256, [0, 1024, 2048, 512], [512] * 4, {}, 2048,
+                        torch.float16, 7)
+    kp, vp = p.k_pool.to(dev), p.v_pool.to(dev)
+    args = (p.q.to(dev), kp, vp, p.block_table.to(dev), p.cu_q.to(dev), p.seq_lens.to(dev),
+            p.max_q_len, p.max_seq_len, True)
+    out = torch.empty_like(args[0])
+    us = _graph_us(torch, lambda i: kc.paged_prefill(*args, out=out), 5)
+    tf = wl.prefill_flops(p) / (us * 1e-6) / 1e12
+    res["head_dim256_prefill_fp16"] = {"us": round(us, 1), "TFLOPs": round(tf, 1),
+                                       "mfma_frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4)}
     return res
 
 
