@@ -240,8 +240,8 @@ int llkv_paged_prefill(void* out, const void* q, const void* k_pool,
  * Hkv*D, as EngineServer::step builds them, engine_server.cpp:1635-1636).
  * max_tokens is a host upper bound of num_tokens[e] (0: P_total; a tight
  * bound avoids launching empty query blocks).  16-byte aligned buffers with
- * head_dim 64, 128 or 256 run on the MFMA prefill kernels; other shapes on a
- * row kernel.  Unlike the reference
+ * head_dim 64, 96, 128 or 256 run on the MFMA prefill kernels; other shapes
+ * on a row kernel.  Unlike the reference
  * this does not synchronise. */
 int llkv_first_prefill_batched(void* out, const void* q, const void* k,
                                const void* v, int num_q_heads,

@@ -139,12 +139,14 @@ template <int D> struct ScoreOps<bf16_t, D> : ScoreOps16<bf16_t, D> {};
 template <typename TT, int D, int G, bool A = false>
 struct MfmaDecode {
     static_assert(G >= 1 && G <= 16, "up to 16 query heads per KV head");
-    static_assert(D % 64 == 0, "head_dim multiple of 64");
+    static_assert(D % 32 == 0, "head_dim multiple of 32");
     using T = TT;
     using Ops = ScoreOps<T, D>;
     static constexpr int W = kDecodeWaves;    // waves per work-group
-    static constexpr int DT = D / 16;         // 16-dim tiles of O^T
-    static constexpr int VH = D / 64;         // 16-byte V vectors per lane per token
+    // V is loaded in 64-dim groups (h), lane c holding dims 64h + 4c .. + 3;
+    // with head_dim 96 the last group is half empty (lanes c >= 8 load none).
+    static constexpr int VH = (D + 63) / 64;  // V vectors per lane per token
+    static constexpr int DT = 4 * VH;         // O^T tiles (tile 4h + j: dims 64h + 4r + j)
     static constexpr int MD = (D + 63) / 64;
     static constexpr int GQ = G, HD = D;
     // 16-bit pools at head_dim 256: O^T = V^T P^T on the 16x16x16 f16 / bf16
@@ -156,7 +158,7 @@ struct MfmaDecode {
     // Resident waves per SIMD the register budget is held to: 5 (<= 96
     // registers) for head_dim 64; head_dim 128 needs more and gets 4.
     // head_dim 256: ~200 VGPRs (two waves per SIMD, no spills; three spill 33-49).
-    static constexpr int kWavesPerEU = D == 64 ? 5 : (D == 128 ? 4 : 2);
+    static constexpr int kWavesPerEU = D == 64 ? 5 : (D == 96 ? 3 : (D == 128 ? 4 : 2));
     // Segments per round: two where the LDS for the parked states stays small.
     static constexpr int kSegMax = G * D <= 512 ? 2 : 1;
 
@@ -216,8 +218,9 @@ struct MfmaDecode {
                 for (int h = 0; h < VH; ++h)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        *reinterpret_cast<float4*>(&sm.acc[s][w][c][64 * h + 16 * g + 4 * i]) =
-                            make_float4(o[4 * h][i], o[4 * h + 1][i], o[4 * h + 2][i], o[4 * h + 3][i]);
+                        if (D % 64 == 0 || 64 * h + 16 * g + 4 * i < D)
+                            *reinterpret_cast<float4*>(&sm.acc[s][w][c][64 * h + 16 * g + 4 * i]) =
+                                make_float4(o[4 * h][i], o[4 * h + 1][i], o[4 * h + 2][i], o[4 * h + 3][i]);
                 if (g == 0) {
                     sm.ml[s][w][c][0] = m;
                     sm.ml[s][w][c][1] = ls;
@@ -277,8 +280,14 @@ struct MfmaDecode {
                 if (newpage && 4 * g + i == snew_r) vp = reinterpret_cast<const T*>(a.vnew) + nrow + 4 * c;
 #pragma unroll
                 for (int h = 0; h < VH; ++h) {
-                    if constexpr (kHalfPV) vh[h][i] = *reinterpret_cast<const mu32x2*>(vp + 64 * h);
-                    else vr[h][i] = Ops::load_v4(vp + 64 * h);
+                    if (D % 64 != 0 && 64 * h + 4 * c >= D) {   // past the head's last dim
+                        vh[h][i] = mu32x2{0u, 0u};
+                        vr[h][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    } else if constexpr (kHalfPV) {
+                        vh[h][i] = *reinterpret_cast<const mu32x2*>(vp + 64 * h);
+                    } else {
+                        vr[h][i] = Ops::load_v4(vp + 64 * h);
+                    }
                 }
             }
             // The fused variant's pointer selects make the scheduler sink the V
@@ -364,6 +373,7 @@ struct MfmaDecode {
 #pragma unroll
                 for (int i = 0; i < MD; ++i) {
                     const int dd = lane + 64 * i;
+                    if (D % 64 != 0 && dd >= D) break;
                     float ov = 0.0f;
 #pragma unroll
                     for (int ww = 0; ww < W; ++ww) ov = fmaf(f[ww], sm.acc[s][ww][h][dd], ov);

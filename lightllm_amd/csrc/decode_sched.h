@@ -126,14 +126,15 @@ Kernels tuned_g(int G) {
     return Kernels();
 }
 
-// head_dim 256 (Gemma-2 / Gemma-3 layouts): group sizes 1, 2, 4, 8, two waves per SIMD.
-template <typename T, bool A>
-Kernels tuned_g256(int G) {
+// head_dim 96 (Phi-3 layouts) and 256 (Gemma-2 / Gemma-3 layouts): group
+// sizes 1, 2, 4, 8.
+template <typename T, int D, bool A>
+Kernels tuned_g_few(int G) {
     switch (G) {
-        case 1: return kernels_of<MfmaDecode<T, 256, 1, A>>();
-        case 2: return kernels_of<MfmaDecode<T, 256, 2, A>>();
-        case 4: return kernels_of<MfmaDecode<T, 256, 4, A>>();
-        case 8: return kernels_of<MfmaDecode<T, 256, 8, A>>();
+        case 1: return kernels_of<MfmaDecode<T, D, 1, A>>();
+        case 2: return kernels_of<MfmaDecode<T, D, 2, A>>();
+        case 4: return kernels_of<MfmaDecode<T, D, 4, A>>();
+        case 8: return kernels_of<MfmaDecode<T, D, 8, A>>();
     }
     return Kernels();
 }
@@ -143,7 +144,8 @@ Kernels tuned(int D, int G, bool append) {
     if (D == 64) return append ? tuned_g<T, 64, true>(G) : tuned_g<T, 64, false>(G);
     if (D == 128) return append ? tuned_g<T, 128, true>(G) : tuned_g<T, 128, false>(G);
 #if LLKV_DECODE_D256
-    if (D == 256) return append ? tuned_g256<T, true>(G) : tuned_g256<T, false>(G);
+    if (D == 256) return append ? tuned_g_few<T, 256, true>(G) : tuned_g_few<T, 256, false>(G);
+    if (D == 96) return append ? tuned_g_few<T, 96, true>(G) : tuned_g_few<T, 96, false>(G);
 #endif
     return Kernels();
 }

@@ -3,7 +3,7 @@
 //
 // Kernels:
 //  * prefill_mfma_kernel / prefill_f32_kernel (prefill_mfma.hip): fp16/bf16
-//    and fp32 at head_dim 64/128/256, 16-token pages -- MFMA QK^T and PV
+//    and fp32 at head_dim 64/96/128/256, 16-token pages -- MFMA QK^T and PV
 //    tiles; the fast path.
 //  * rows_generic_kernel (this file): any dtype, any head_dim <= 256, any
 //    page size, paged or contiguous K/V.  One wave per (query row, q_head),

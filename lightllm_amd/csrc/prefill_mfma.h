@@ -1,5 +1,5 @@
 // MFMA paged prefill attention for gfx950 (fp16 / bf16 here; fp32 pools take
-// a 16x16x4 f32 variant of the same schedule; head_dim 64 / 128 / 256,
+// a 16x16x4 f32 variant of the same schedule; head_dim 64 / 96 / 128 / 256,
 // 16-token pages).  Replaces the reference's scalar prefill kernels
 // (src/kv_cache/paged_attention.cu:641-974) for these shapes.
 //

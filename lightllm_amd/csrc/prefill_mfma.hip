@@ -247,7 +247,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     constexpr int DT = D / 16;            // 16-dim tiles of the output
     constexpr int KCH = BN * D / 8;       // 16-byte K chunks per tile
     constexpr int KCH_T = KCH / 256;      // per thread
-    constexpr int VT_T = (BN / 2) * (D / 8) / 256;   // V tasks (2 keys x 8 dims) per thread
+    constexpr int VT_N = (BN / 2) * (D / 8);          // V tasks (2 keys x 8 dims) per tile
+    constexpr int VT_T = (VT_N + 255) / 256;          // per thread (head_dim 96: the last partly idle)
     __shared__ Smem<D> sm;
 
     const int tid = threadIdx.x;
@@ -330,7 +331,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < VT_T; ++j) {
-        const int task = tid + 256 * j;
+        const int task = (VT_N % 256 == 0 || tid + 256 * j < VT_N) ? tid + 256 * j : 0;   // idle: task 0's rows
         const int kp = task % (BN / 2), c = task / (BN / 2);
         vslot[j] = CG ? 2 * kp : (2 * kp) >> 4;
         voff[j] = (CG ? 0u : (uint32_t)((2 * kp) & 15) * row_bytes) + (uint32_t)c * 16u;
@@ -376,6 +377,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 #pragma unroll
         for (int j = 0; j < VT_T; ++j) {
             const int task = tid + 256 * j;
+            if (VT_N % 256 != 0 && task >= VT_N) break;
             const int kp = task % (BN / 2), c = task / (BN / 2);
             // keys 2kp (v0) and 2kp+1 (v1), dims 8c..8c+7: dim e's pair (v0[e], v1[e]) is one
             // dword of V^T, built with v_perm_b32 (low halves: 0x05040100, high: 0x07060302)
@@ -660,7 +662,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 template <int D>
 struct SmemF32 {
     static constexpr int KNB = D == 64 ? LLKV_F32_KNB64 : (D == 128 ? LLKV_F32_KNB128 : 1);
-    static constexpr int VNB = D == 64 ? LLKV_F32_VNB64 : (D == 128 ? LLKV_F32_VNB128 : 1);
+    static constexpr int VNB = D == 64 ? LLKV_F32_VNB64 : (D == 128 ? LLKV_F32_VNB128 : 1);   // 96, 256: 1
     static constexpr int KPAD = D + 4;    // floats per K row (pad: 16-byte reads of 16 rows hit distinct banks)
     static constexpr int VPAD = BN + 4;   // floats per V^T row
     union {
@@ -674,14 +676,15 @@ struct SmemF32 {
 };
 
 template <int D, bool CG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? LLKV_F32_WPE64 : LLKV_F32_WPE128)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? LLKV_F32_WPE64 : (D == 96 ? 2 : LLKV_F32_WPE128))))
 void prefill_f32_kernel(MfmaPrefillArgs a) {
     typedef SmemF32<D> S;
     constexpr int KPAD = S::KPAD, VPAD = S::VPAD, KNB = S::KNB, VNB = S::VNB;
     constexpr int KB = D / 16;              // 16-dim blocks of the QK^T product
     constexpr int DT = D / 16;              // 16-dim tiles of the output
     constexpr int KCH_T = BN * D / 4 / 256;          // 16-byte K chunks per thread
-    constexpr int VT_T = (BN / 4) * (D / 4) / 256;   // V tasks (4 keys x 4 dims) per thread
+    constexpr int VT_N = (BN / 4) * (D / 4);           // V tasks (4 keys x 4 dims) per tile
+    constexpr int VT_T = (VT_N + 255) / 256;           // per thread (head_dim 96: the last partly idle)
     __shared__ S sm;
 
     const int tid = threadIdx.x;
@@ -745,7 +748,7 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < VT_T; ++j) {
-        const int task = tid + 256 * j;
+        const int task = (VT_N % 256 == 0 || tid + 256 * j < VT_N) ? tid + 256 * j : 0;   // idle: task 0's rows
         const int kq = task % (BN / 4), c = task / (BN / 4);   // keys 4kq .. 4kq+3, dims 4c .. 4c+3
         vslot[j] = CG ? 4 * kq : (4 * kq) >> 4;
         voff[j] = (CG ? 0u : (uint32_t)((4 * kq) & 15) * row_bytes) + (uint32_t)c * 16u;
@@ -798,6 +801,7 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
 #pragma unroll
         for (int j = 0; j < VT_T; ++j) {
             const int task = tid + 256 * j;
+            if (VT_N % 256 != 0 && task >= VT_N) break;
             const int kq = task % (BN / 4), c = task / (BN / 4);
 #pragma unroll
             for (int e = 0; e < 4; ++e)   // 4x4 transpose: V^T row 4c + e, keys 4kq .. 4kq+3
@@ -1044,7 +1048,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
 
 bool prefill_mfma_handles(int head_dim, int block_size, int dtype) {
     // head_dim 256: one work-group per CU (fp32: single-buffered tiles, 134 KB)
-    return block_size == kPage && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+    return block_size == kPage && (head_dim == 64 || head_dim == 96 || head_dim == 128 || head_dim == 256);
 }
 
 // Key-range split.  When the (sequence, query block, q head) units alone
@@ -1065,37 +1069,51 @@ constexpr int kSizingSlots = 1024;
 
 typedef void (*PrefillFn)(MfmaPrefillArgs);
 
+template <typename T, bool CG>
+PrefillFn kernel16(int head_dim) {
+    switch (head_dim) {
+        case 64: return prefill_mfma_kernel<T, 64, CG>;
+        case 96: return prefill_mfma_kernel<T, 96, CG>;
+        case 128: return prefill_mfma_kernel<T, 128, CG>;
+        default: return prefill_mfma_kernel<T, 256, CG>;
+    }
+}
+
+template <bool CG>
+PrefillFn kernel32(int head_dim) {
+    switch (head_dim) {
+        case 64: return prefill_f32_kernel<64, CG>;
+        case 96: return prefill_f32_kernel<96, CG>;
+        case 128: return prefill_f32_kernel<128, CG>;
+        default: return prefill_f32_kernel<256, CG>;
+    }
+}
+
 template <bool CG>
 PrefillFn prefill_kernel_cg(int dtype, int head_dim) {
-    if (dtype == LLKV_DTYPE_F32)
-        return head_dim == 64    ? prefill_f32_kernel<64, CG>
-               : head_dim == 128 ? prefill_f32_kernel<128, CG>
-                                 : prefill_f32_kernel<256, CG>;
-    if (dtype == LLKV_DTYPE_F16)
-        return head_dim == 64    ? prefill_mfma_kernel<_Float16, 64, CG>
-               : head_dim == 128 ? prefill_mfma_kernel<_Float16, 128, CG>
-                                 : prefill_mfma_kernel<_Float16, 256, CG>;
-    return head_dim == 64    ? prefill_mfma_kernel<bf16_t, 64, CG>
-           : head_dim == 128 ? prefill_mfma_kernel<bf16_t, 128, CG>
-                             : prefill_mfma_kernel<bf16_t, 256, CG>;
+    if (dtype == LLKV_DTYPE_F32) return kernel32<CG>(head_dim);
+    if (dtype == LLKV_DTYPE_F16) return kernel16<_Float16, CG>(head_dim);
+    return kernel16<bf16_t, CG>(head_dim);
 }
 
 PrefillFn prefill_kernel(int dtype, int head_dim, bool contig) {
     return contig ? prefill_kernel_cg<true>(dtype, head_dim) : prefill_kernel_cg<false>(dtype, head_dim);
 }
 
+template <typename T>
+PrefillFn merge_for(int head_dim) {
+    switch (head_dim) {
+        case 64: return prefill_merge_kernel<T, 64>;
+        case 96: return prefill_merge_kernel<T, 96>;
+        case 128: return prefill_merge_kernel<T, 128>;
+        default: return prefill_merge_kernel<T, 256>;
+    }
+}
+
 PrefillFn merge_kernel(int dtype, int head_dim) {
-    if (dtype == LLKV_DTYPE_F32)
-        return head_dim == 64    ? prefill_merge_kernel<float, 64>
-               : head_dim == 128 ? prefill_merge_kernel<float, 128>
-                                 : prefill_merge_kernel<float, 256>;
-    if (dtype == LLKV_DTYPE_F16)
-        return head_dim == 64    ? prefill_merge_kernel<_Float16, 64>
-               : head_dim == 128 ? prefill_merge_kernel<_Float16, 128>
-                                 : prefill_merge_kernel<_Float16, 256>;
-    return head_dim == 64    ? prefill_merge_kernel<bf16_t, 64>
-           : head_dim == 128 ? prefill_merge_kernel<bf16_t, 128>
-                             : prefill_merge_kernel<bf16_t, 256>;
+    if (dtype == LLKV_DTYPE_F32) return merge_for<float>(head_dim);
+    if (dtype == LLKV_DTYPE_F16) return merge_for<_Float16>(head_dim);
+    return merge_for<bf16_t>(head_dim);
 }
 
 struct ChunkPlan {

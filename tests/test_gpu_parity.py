@@ -221,6 +221,7 @@ FUSED = [
     ("f16_G6_D128_auto", 48, 12, 2, 128, torch.float16, 0, (1, 3000)),
     ("f32_G5_S3", 20, 10, 2, 64, torch.float32, 3, (1, 900)),
     ("f16_D256_G2_auto", 24, 16, 8, 256, torch.float16, 0, (1, 2500)),
+    ("f32_D96_MHA_auto", 30, 8, 8, 96, torch.float32, 0, (1, 1200)),
 ]
 
 
@@ -401,6 +402,10 @@ EDGE = [
     ("fp16_D256_g2", 16, 8, 256, [1, 129, 1500], torch.float16),
     ("bf16_D256_g8", 8, 1, 256, [40, 700], torch.bfloat16),
     ("fp32_D256_g1", 4, 4, 256, [17, 333], torch.float32),
+    # head_dim 96 (Phi-3 heads: 32 / 32, multi-head) on the MFMA body, half-empty last V group
+    ("fp16_D96_mha", 8, 8, 96, [1, 300, 1100], torch.float16),
+    ("fp32_D96_g2", 8, 4, 96, [15, 16, 17, 640], torch.float32),
+    ("bf16_D96_g4", 8, 2, 96, [90, 1500], torch.bfloat16),
     ("gqa_8_2", 8, 2, 64, [200, 33], torch.float32),
     ("mqa_hkv1", 8, 1, 64, [200, 33], torch.float32),
     ("mha", 4, 4, 64, [200, 33], torch.float32),
@@ -575,6 +580,11 @@ PREFILL = [
     ("bf16_D256_long_noncausal", 8, 4, 256, [2200], [90], torch.bfloat16, False),
     ("fp32_D256", 4, 2, 256, [40, 900], [33, 150], torch.float32, True),
     ("fp32_D256_long", 8, 4, 256, [2300], [70], torch.float32, True),
+    # head_dim 96 (Phi-3): 1.5 V staging tasks per thread
+    ("fp16_D96", 8, 8, 96, [0, 300], [200, 77], torch.float16, True),
+    ("bf16_D96_long", 8, 8, 96, [2300, 10], [70, 129], torch.bfloat16, True),
+    ("fp32_D96", 8, 4, 96, [40, 700], [33, 150], torch.float32, True),
+    ("fp32_D96_long_noncausal", 4, 4, 96, [2200], [60], torch.float32, False),
 ]
 
 
@@ -636,6 +646,7 @@ FIRST = [
      torch.float32, True),
     ("fp32_generic_D67", 4, 2, 67, [33, 100], [0, 2], torch.float32, False),
     ("fp16_D256", 16, 8, 256, [300, 41], [0, 5], torch.float16, True),
+    ("fp32_D96_mha", 8, 8, 96, [300, 41, 129], [0, 5, 2], torch.float32, True),
     # more than 1024 (entry, query block) units: index order instead of the longest-first ranking
     ("fp16_1200_units", 4, 2, 64, [(37 * i) % 250 + 1 for i in range(600)], [0] * 600, torch.float16,
      True),
