@@ -18,7 +18,7 @@ struct Kernels {
 // Tuned kernels for head_dim D and G query heads per kv head, plain or with
 // the fused append of the step's new row; both null when the shape has no
 // tuned body (the dispatcher then runs the generic kernel).  Tuned: D 64 or
-// 128 with G in {1, 2, 3, 4, 5, 6, 7, 8, 16}; D 96 or 256 with G in {1, 2, 4, 8}.
+// 128 with G in {1, 2, 3, 4, 5, 6, 7, 8, 12, 16}; D 96 or 256 with G in {1, 2, 4, 8}.
 Kernels tuned_kernels_f32(int D, int G, bool append);
 Kernels tuned_kernels_f16(int D, int G, bool append);
 Kernels tuned_kernels_bf16(int D, int G, bool append);

@@ -121,6 +121,7 @@ Kernels tuned_g(int G) {
         case 6: return kernels_of<MfmaDecode<T, D, 6, A>>();
         case 7: return kernels_of<MfmaDecode<T, D, 7, A>>();
         case 8: return kernels_of<MfmaDecode<T, D, 8, A>>();
+        case 12: return kernels_of<MfmaDecode<T, D, 12, A>>();
         case 16: return kernels_of<MfmaDecode<T, D, 16, A>>();
     }
     return Kernels();

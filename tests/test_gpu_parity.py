@@ -416,7 +416,9 @@ EDGE = [
     ("fp32_D128_g6", 12, 2, 128, [5, 640, 1500], torch.float32),
     ("bf16_D64_g6", 12, 2, 64, [31, 900], torch.bfloat16),
     ("fp32_D64_g5", 10, 2, 64, [64, 1029], torch.float32),
-    ("gqa_g12_generic", 12, 1, 64, [130, 5], torch.float32),
+    ("gqa_g12", 12, 1, 64, [130, 5], torch.float32),
+    ("fp16_D128_g12", 48, 4, 128, [3, 700, 1900], torch.float16),   # StarCoder2-15B heads
+    ("gqa_g10_generic", 10, 1, 64, [130, 5], torch.float32),
     ("fp16_D128_g4", 32, 8, 128, [1, 500, 2049], torch.float16),
     ("fp16_D64_g7", 14, 2, 64, [7, 700], torch.float16),
     ("bf16_D64_g7", 14, 2, 64, [7, 700], torch.bfloat16),
