@@ -42,7 +42,6 @@ struct Scratch {
         ptr = nullptr;
         bytes = 0;
         hip_throw(hipMalloc(&ptr, need), "hipMalloc(workspace)");
-        hip_throw(hipMemset(ptr, 0, need), "hipMemset(workspace)");
         bytes = need;
         return ptr;
     }
@@ -201,15 +200,16 @@ void first_prefill_attn_batched_gpu_dispatch(DType dtype, void* out_ptr, const v
                                              const int* token_cumsum, const int* start_poss,
                                              int N, int P_total, float scale) {
     if (D > 256) throw std::runtime_error("first_prefill_attn_batched: head_dim too large");
-    // The longest entry bounds the query blocks of the launch (P_total would
-    // launch mostly empty work-groups): one small device-to-host read, in a
-    // call that synchronises anyway.
+    // The longest entry (query rows token_cumsum[e + 1] - token_cumsum[e])
+    // bounds the query blocks of the launch; P_total would launch mostly empty
+    // work-groups.  One device-to-host read of N + 1 ints before the launch,
+    // which the reference does not make; its call synchronises at the end.
     int max_tokens = 0;
-    if (N > 0 && num_tokens != nullptr) {
-        std::vector<int> nt(N);
-        hip_throw(hipMemcpy(nt.data(), num_tokens, N * sizeof(int), hipMemcpyDeviceToHost),
+    if (N > 0 && token_cumsum != nullptr) {
+        std::vector<int> tc(N + 1);
+        hip_throw(hipMemcpy(tc.data(), token_cumsum, (N + 1) * sizeof(int), hipMemcpyDeviceToHost),
                   "first_prefill_attn_batched");
-        max_tokens = *std::max_element(nt.begin(), nt.end());
+        for (int e = 0; e < N; ++e) max_tokens = std::max(max_tokens, tc[e + 1] - tc[e]);
         if (max_tokens <= 0) max_tokens = P_total;
     }
     throw_if(llkv_first_prefill_batched(out_ptr, q_ptr, k_ptr, v_ptr, Hq, Hkv, D, offsets, kv_offsets,

@@ -261,6 +261,7 @@ extern "C" int llkv_first_prefill_batched(void* out, const void* q, const void* 
     m.q_off = offsets;
     m.kv_off = kv_offsets;
     m.ntok = num_tokens;
+    m.tcum = token_cumsum;
     m.q_row = num_q_heads * head_dim;
     const int r = launch_prefill_mfma(m, head_dim, kPage, dtype, P_total, bound, bound, nullptr, 0,
                                       (hipStream_t)stream);

@@ -42,13 +42,15 @@ struct MfmaPrefillArgs {
     const int* cu_q;
     const int* lens;
     int max_blocks, N, Hq, Hkv, causal;
-    // contiguous K/V (first prefill): sequence n's q rows start at element
-    // q_off[n] (a multiple of q_row = Hq * D), its num_tokens ntok[n] keys at
-    // element kv_off[n] of k / v; cu_q, lens and bt are unused.
+    // contiguous K/V (first prefill): entry n's tcum[n + 1] - tcum[n] q rows
+    // start at element q_off[n] (a multiple of q_row = Hq * D), its ntok[n]
+    // keys at element kv_off[n] of k / v, and query row i sees keys j <= i
+    // (paged_attention.cu:1253-1285); cu_q, lens and bt are unused.
     int contig;
     const int* q_off;
     const int* kv_off;
     const int* ntok;
+    const int* tcum;
     int q_row;
     float scale_log2;
     int qblocks;      // query blocks per sequence

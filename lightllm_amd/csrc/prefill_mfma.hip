@@ -56,19 +56,25 @@ constexpr int BN = 64;    // keys per tile (four pages)
 // key tiles (the causal extent of the rows).  Query blocks are numbered from
 // the last, so that in a sequence the longest unit comes first.
 struct UnitInfo {
-    int q0, P, L, kvo, tiles;
+    int q0, P, L, kvo, hist, tiles;
 };
 
 // Sequence n's first q row, new tokens P, keys L, and (contiguous K/V) the
 // element offset of its first K/V row.  Paged: rows cu_q[n] .. cu_q[n+1],
 // L = seq_lens[n] capped at the table's extent.  Contiguous (first prefill):
-// q rows from offsets[n] (a row start), P = L = num_tokens[n].
-__device__ inline void seq_geom(const MfmaPrefillArgs& a, int n, int& q0, int& P, int& L, int& kvo) {
+// q rows from offsets[n] (a row start), P = token_cumsum[n + 1] - token_cumsum[n],
+// L = num_tokens[n].
+// hist: keys before query row 0's own position, so that causal query row i
+// sees keys j <= hist + i (L - P for a chunk on a cached prefix; 0 for a first
+// prefill entry, whose query and key counts may differ).
+__device__ inline void seq_geom(const MfmaPrefillArgs& a, int n, int& q0, int& P, int& L, int& kvo,
+                                int& hist) {
     if (a.contig) {
         q0 = a.q_off[n] / a.q_row;
-        P = max(a.ntok[n], 0);
-        L = P;
+        P = max(a.tcum[n + 1] - a.tcum[n], 0);
+        L = max(a.ntok[n], 0);
         kvo = a.kv_off[n];
+        hist = 0;
     } else {
         q0 = a.cu_q[n];
         P = a.cu_q[n + 1] - q0;
@@ -76,6 +82,7 @@ __device__ inline void seq_geom(const MfmaPrefillArgs& a, int n, int& q0, int& P
         const int cap = a.max_blocks * kPage;
         L = l < 0 ? 0 : (l > cap ? cap : l);
         kvo = 0;
+        hist = L - P;
     }
 }
 
@@ -83,13 +90,13 @@ __device__ inline UnitInfo unit_info(const MfmaPrefillArgs& a, int u) {
     const int n = u / a.qblocks;
     const int qb = a.qblocks - 1 - (u % a.qblocks);
     UnitInfo r;
-    seq_geom(a, n, r.q0, r.P, r.L, r.kvo);
+    seq_geom(a, n, r.q0, r.P, r.L, r.kvo, r.hist);
     const int q_lo = qb * BQ;
     if (q_lo >= r.P) {
         r.tiles = 0;
         return r;
     }
-    int kend = a.causal ? r.L - r.P + min(q_lo + BQ, r.P) : r.L;
+    int kend = a.causal ? r.hist + min(q_lo + BQ, r.P) : r.L;
     kend = kend < 0 ? 0 : (kend > r.L ? r.L : kend);
     r.tiles = (kend + BN - 1) / BN;
     return r;
@@ -179,7 +186,7 @@ constexpr int kXcds = 8;   // XCDs of an MI355X; work-groups go to them round-ro
 // j (slot-major) goes to XCD j % 8 with its G heads as that XCD's next G
 // work-groups: they run together and share their K/V reads in one L2.
 struct Work {
-    int hq, kvh, unit, n, ci, q0, P, q_lo, L, kvo, kend, t_begin, t_end;
+    int hq, kvh, unit, n, ci, q0, P, q_lo, L, kvo, hist, kend, t_begin, t_end;
     bool direct;   // one chunk: write the output row itself
 };
 
@@ -212,15 +219,34 @@ __device__ inline bool take_work(const MfmaPrefillArgs& a, int* order, Work& wk)
     if (wk.q_lo >= wk.P) return false;
     wk.L = ui.L;
     wk.kvo = ui.kvo;
-    int kend = a.causal ? wk.L - wk.P + min(wk.q_lo + BQ, wk.P) : wk.L;
+    wk.hist = a.contig ? 0 : ui.L - ui.P;   // as seq_geom (not kept with the ranked units)
+    int kend = a.causal ? wk.hist + min(wk.q_lo + BQ, wk.P) : wk.L;
     wk.kend = kend < 0 ? 0 : (kend > wk.L ? wk.L : kend);
     const int ntiles = (wk.kend + BN - 1) / BN;
-    const int nchunks = (ntiles + a.chunk_tiles - 1) / a.chunk_tiles;
+    // at most max_chunks chunks (a max_seq_len bound below a length): the last
+    // one takes the remaining tiles
+    const int nchunks = min((ntiles + a.chunk_tiles - 1) / a.chunk_tiles, a.max_chunks);
     if (wk.ci > 0 && wk.ci >= nchunks) return false;   // chunk 0 also covers an empty key range (zeros)
     wk.t_begin = wk.ci * a.chunk_tiles;
-    wk.t_end = min(wk.t_begin + a.chunk_tiles, ntiles);
+    wk.t_end = wk.ci == nchunks - 1 ? ntiles : min(wk.t_begin + a.chunk_tiles, ntiles);
     wk.direct = nchunks <= 1;
     return true;
+}
+
+// Query rows beyond the launch's qblocks * BQ (a max_q_len bound below a
+// sequence's query count) have no work-group: the top query block's chunk-0
+// work-group sets them to NaN for its head, so the broken bound shows in the
+// output instead of leaving stale rows.
+template <typename T, int D>
+__device__ inline void poison_uncovered_rows(const MfmaPrefillArgs& a, const Work& wk) {
+    const int covered = a.qblocks * BQ;
+    if (wk.ci != 0 || wk.q_lo != covered - BQ || wk.P <= covered) return;
+    T* og = reinterpret_cast<T*>(a.out);
+    const int n = (wk.P - covered) * D;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int r = covered + i / D;
+        og[((int64_t)(wk.q0 + r) * a.Hq + wk.hq) * D + i % D] = Elem<T>::from_f32(__builtin_nanf(""));
+    }
 }
 
 template <int D>
@@ -257,6 +283,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const int g = lane >> 4, c16 = lane & 15;
     Work wk;
     if (!take_work(a, sm.order, wk)) return;
+    poison_uncovered_rows<T, D>(a, wk);
     const int hq = wk.hq, kvh = wk.kvh, unit = wk.unit, n = wk.n, ci = wk.ci;
     const int q0 = wk.q0, P = wk.P, q_lo = wk.q_lo, L = wk.L, kend = wk.kend;
     const int t_begin = wk.t_begin, t_end = wk.t_end;
@@ -290,13 +317,13 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int ql = q_lo + w * WQ + nt * 16 + c16;
-        qpos[nt] = ql < P ? (a.causal ? L - P + ql : L - 1) : -1;
+        qpos[nt] = ql < P ? (a.causal ? wk.hist + ql : L - 1) : -1;
     }
 
     // Smallest query position of the wave's 32 rows (every row valid), for the
     // unmasked fast path of tiles that lie entirely below it.
     const int wq0 = q_lo + w * WQ;
-    const int wave_min_pos = (wq0 + WQ <= P) ? (a.causal ? L - P + wq0 : L - 1) : -1;
+    const int wave_min_pos = (wq0 + WQ <= P) ? (a.causal ? wk.hist + wq0 : L - 1) : -1;
 
     f32x4 o[DT][2];
 #pragma unroll
@@ -693,6 +720,7 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
     const int g = lane >> 4, c16 = lane & 15;
     Work wk;
     if (!take_work(a, sm.order, wk)) return;
+    poison_uncovered_rows<float, D>(a, wk);
     const int hq = wk.hq, kvh = wk.kvh, unit = wk.unit, n = wk.n, ci = wk.ci;
     const int q0 = wk.q0, P = wk.P, q_lo = wk.q_lo, L = wk.L, kend = wk.kend;
     const int t_begin = wk.t_begin, t_end = wk.t_end;
@@ -716,10 +744,10 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int ql = q_lo + w * WQ + nt * 16 + c16;
-        qpos[nt] = ql < P ? (a.causal ? L - P + ql : L - 1) : -1;
+        qpos[nt] = ql < P ? (a.causal ? wk.hist + ql : L - 1) : -1;
     }
     const int wq0 = q_lo + w * WQ;
-    const int wave_min_pos = (wq0 + WQ <= P) ? (a.causal ? L - P + wq0 : L - 1) : -1;
+    const int wave_min_pos = (wq0 + WQ <= P) ? (a.causal ? wk.hist + wq0 : L - 1) : -1;
 
     f32x4 o[DT][2];
 #pragma unroll
@@ -992,15 +1020,15 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
     const int hq = blockIdx.x, unit = blockIdx.y;
     const int n = unit / a.qblocks;
     const int qb = a.qblocks - 1 - (unit % a.qblocks);
-    int q0, P, L, kvo;
-    seq_geom(a, n, q0, P, L, kvo);
+    int q0, P, L, kvo, hist;
+    seq_geom(a, n, q0, P, L, kvo, hist);
     const int q_lo = qb * BQ;
     const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
     if (q_lo + row >= P) return;
-    int kend = a.causal ? L - P + min(q_lo + BQ, P) : L;
+    int kend = a.causal ? hist + min(q_lo + BQ, P) : L;
     kend = kend < 0 ? 0 : (kend > L ? L : kend);
     const int ntiles = (kend + BN - 1) / BN;
-    const int nchunks = (ntiles + a.chunk_tiles - 1) / a.chunk_tiles;
+    const int nchunks = min((ntiles + a.chunk_tiles - 1) / a.chunk_tiles, a.max_chunks);   // as take_work
     if (nchunks <= 1) return;   // written directly
     const int64_t p0 = ((int64_t)unit * a.max_chunks) * a.Hq + hq;   // chunk c at p0 + c * Hq
     float M = -INFINITY, W = 0.0f;

@@ -44,16 +44,37 @@ def check_fp32(got: torch.Tensor, ref: np.ndarray, what: str, rtol=1e-5, atol=1e
     assert np.all(err <= bound), f"{what}: {int((err > bound).sum())} elements out of tolerance"
 
 
-def check_lowp(got: torch.Tensor, ref: np.ndarray, what: str, rtol: float):
+def lowp_stats(got: np.ndarray, ref: np.ndarray):
+    """Plain statistics of a 16-bit result: the worst per-row max|err| / max|ref|, and the
+    worst elementwise relative error over elements with |ref| >= 0.1 * RMS of their row."""
+    err = np.abs(got - ref)
+    rowmax = np.abs(ref).max(axis=-1)
+    row_ratio = np.divide(err.max(axis=-1), rowmax, out=np.zeros_like(rowmax), where=rowmax > 0)
+    rms = np.sqrt(np.mean(ref ** 2, axis=-1, keepdims=True))
+    big = np.abs(ref) >= 0.1 * rms
+    rel = np.divide(err, np.abs(ref), out=np.zeros_like(err), where=big & (ref != 0))
+    return float(row_ratio.max()) if row_ratio.size else 0.0, float(rel.max()) if rel.size else 0.0
+
+
+def check_lowp(got: torch.Tensor, ref: np.ndarray, what: str, rtol: float, plain: bool = False):
+    """Row-RMS bar (module docstring), and the two plain statistics of lowp_stats printed.
+    plain=True (configurations 3-5) also asserts the per-row max|err| / max|ref| <= rtol.  The
+    elementwise relative error at |ref| >= 0.1 RMS is reported, not asserted: the prefill
+    kernels round the softmax weights P to fp16 for the PV product (as flash attention does),
+    an error of ~2^-11 of the row's magnitude, which is ~5e-3 of an element at 0.1 RMS."""
     g = f64(got)
     err = np.abs(g - ref)
     # relative to each output vector's RMS (over head_dim), plus the element itself
     rms = np.sqrt(np.mean(ref ** 2, axis=-1, keepdims=True))
     bound = rtol * (np.abs(ref) + rms)
     ratio = np.divide(err, bound, out=np.where(err > 0, np.inf, 0.0), where=bound > 0)
+    row_ratio, rel = lowp_stats(g, ref)
     say(f"  {what}: max abs err {float(err.max()):.3e}, "
-        f"worst err/bound {float(ratio.max()):.3f}")
+        f"worst err/bound {float(ratio.max()):.3f}, row max|err|/max|ref| {row_ratio:.2e}, "
+        f"elementwise rel (|ref| >= 0.1 rms) {rel:.2e}")
     assert np.all(err <= bound), f"{what}: {int((err > bound).sum())} elements out of tolerance"
+    if plain:
+        assert row_ratio <= rtol, f"{what}: row max|err|/max|ref| {row_ratio:.3e} > {rtol}"
 
 
 def bits(t: torch.Tensor) -> np.ndarray:
@@ -384,7 +405,7 @@ def test_decode_config3_fp16_splitk(splits):
     case = wl.config3()
     out, _, _ = run_decode(case, num_splits=splits, append=False)
     ref = oracle_decode(case, np_pool(case.k_pool), np_pool(case.v_pool), threads=16)
-    check_lowp(out, ref, f"cfg3 decode S={splits}", 2e-3)
+    check_lowp(out, ref, f"cfg3 decode S={splits}", 2e-3, plain=True)
 
 
 EDGE = [
@@ -538,7 +559,7 @@ def test_prefill_config4_fp16():
     case = wl.config4()
     out, kp, vp = run_prefill(case)
     ref = oracle_prefill(case, kp, vp)
-    check_lowp(out, ref, "cfg4 prefill", 2e-3)
+    check_lowp(out, ref, "cfg4 prefill", 2e-3, plain=True)
 
 
 def test_prefill_config4_unsplit_workspace():
@@ -635,6 +656,95 @@ def test_prefill_loose_bounds(dtype):
         return
     check_lowp(loose, ref, "prefill loose bounds", 2e-3 if dtype == torch.float16 else 1.6e-2)
     check_lowp(tight, ref, "prefill tight bounds", 2e-3 if dtype == torch.float16 else 1.6e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_prefill_undersized_bounds(dtype):
+    """Host bounds below the actual lengths.  A max_seq_len bound below a sequence's length
+    plans fewer key chunks: the last chunk takes the remaining keys and the result is
+    unchanged.  A max_q_len bound below a chunk's query count leaves rows with no
+    work-group: they come out NaN (the broken bound shows), every other row is right, and
+    nothing is read or written out of bounds."""
+    say(f"prefill with undersized max_q_len / max_seq_len bounds {dtype}")
+    prefixes, chunks = [3000, 0, 1500], [64, 300, 129]
+    nb = sum((p + c + 15) // 16 for p, c in zip(prefixes, chunks)) + 4
+    case = wl.prefill_case("short", 14, 2, 64, prefixes, chunks, {}, nb, dtype, seed=78)
+    kp, vp = case.k_pool.to(DEV), case.v_pool.to(DEV)
+    kc.append_kv(case.k_chunk.to(DEV), case.v_chunk.to(DEV), case.slots.to(DEV), kp, vp)
+    args = (case.q.to(DEV), kp, vp, case.block_table.to(DEV), case.cu_q.to(DEV), case.seq_lens.to(DEV))
+    short_keys = kc.paged_prefill(*args, case.max_q_len, case.max_seq_len // 8, causal=True,
+                                  scale=case.scale)
+    short_rows = kc.paged_prefill(*args, 100, case.max_seq_len, causal=True, scale=case.scale)
+    torch.cuda.synchronize()
+    ref = oracle_prefill(case, kp, vp)
+    chk = (lambda o, r, w: check_fp32(o, r, w)) if dtype == torch.float32 else \
+          (lambda o, r, w: check_lowp(o, r, w, 2e-3))
+    chk(short_keys, ref, "max_seq_len bound / 8")
+    # rows of each sequence beyond the first 128 (one query block) are NaN, the others right
+    cu = case.cu_q.tolist()
+    covered = np.zeros(ref.shape[0], dtype=bool)
+    for n in range(len(chunks)):
+        covered[cu[n]:cu[n] + min(128, cu[n + 1] - cu[n])] = True
+    got = short_rows.float().cpu().numpy()
+    assert np.isnan(got[~covered]).all(), "uncovered rows are not NaN"
+    chk(short_rows[torch.from_numpy(covered).to(DEV)], ref[covered], "max_q_len bound 100 (covered rows)")
+
+
+def first_prefill_ref(q, k, v, offs_rows, kv_rows, qrows, nkeys, scale):
+    """float64 first prefill following the reference kernel (paged_attention.cu:1253-1285):
+    entry e's query row r (of qrows[e]) attends keys pos <= r with pos < nkeys[e]."""
+    out = {}
+    for e in range(len(qrows)):
+        for r in range(qrows[e]):
+            qr = q[offs_rows[e] + r].astype(np.float64)                       # [Hq, D]
+            nk = min(r + 1, nkeys[e])
+            kk = k[kv_rows[e]:kv_rows[e] + nk].astype(np.float64)              # [nk, Hkv, D]
+            vv = v[kv_rows[e]:kv_rows[e] + nk].astype(np.float64)
+            g = q.shape[1] // k.shape[1]
+            kq = np.repeat(kk, g, axis=1)                                       # [nk, Hq, D]
+            vq = np.repeat(vv, g, axis=1)
+            s = np.einsum("hd,nhd->hn", qr, kq) * scale
+            s -= s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            p /= p.sum(axis=1, keepdims=True)
+            out[offs_rows[e] + r] = np.einsum("hn,nhd->hd", p, vq)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_first_prefill_rows_differ_from_keys(dtype):
+    """Entries whose query rows (token_cumsum[e + 1] - token_cumsum[e]) differ from their key
+    count (num_tokens[e]): row r sees keys pos <= r, pos < num_tokens[e], as the reference
+    kernel maps rows through token_cumsum.  Also pins the oracle's restatement on this case."""
+    say(f"first prefill, query rows != keys {dtype}")
+    hq, hkv, d = 14, 2, 64
+    qrows, nkeys = [40, 300, 7, 129], [100, 150, 7, 300]
+    g = torch.Generator().manual_seed(31)
+    n = len(qrows)
+    cum = np.concatenate([[0], np.cumsum(qrows)]).astype(np.int32)
+    qstart = cum[:-1].astype(np.int32)
+    kvstart = np.concatenate([[0], np.cumsum(nkeys)[:-1]]).astype(np.int32)
+    q = torch.randn(int(cum[-1]), hq, d, generator=g).to(dtype)
+    k = torch.randn(int(sum(nkeys)), hkv, d, generator=g).to(dtype)
+    v = torch.randn(int(sum(nkeys)), hkv, d, generator=g).to(dtype)
+    out = torch.zeros_like(q).to(DEV)
+    t32 = lambda a: torch.as_tensor(a, dtype=torch.int32).to(DEV)
+    scale = 1.0 / math.sqrt(d)
+    kc.first_prefill_attn_batched(out, q.to(DEV), k.to(DEV), v.to(DEV), hq, hkv, d,
+                                  t32(qstart * hq * d), t32(kvstart * hkv * d), t32(nkeys), t32(cum),
+                                  t32(np.zeros(n)), n, int(cum[-1]), scale, max_tokens=max(qrows))
+    torch.cuda.synchronize()
+    qn, kn, vn = q.float().numpy(), k.float().numpy(), v.float().numpy()
+    rows = first_prefill_ref(qn, kn, vn, qstart, kvstart, qrows, nkeys, scale)
+    ref = np.stack([rows[i] for i in range(int(cum[-1]))])
+    if dtype == torch.float32:
+        check_fp32(out, ref, "first prefill rows != keys")
+        r32 = oracle.first_prefill_batched(qn, kn, vn, hq, hkv, d, qstart * hq * d, kvstart * hkv * d,
+                                           np.array(nkeys, np.int32), cum, np.zeros(n, np.int32),
+                                           scale, int(cum[-1]))
+        assert np.all(np.abs(r32 - ref) <= 1e-6 + 1e-5 * np.abs(ref)), "oracle restatement"
+    else:
+        check_lowp(out, ref, "first prefill rows != keys", 2e-3)
 
 
 FIRST = [
@@ -816,6 +926,63 @@ def test_pool_beyond_2pow32_elements():
     torch.cuda.empty_cache()
 
 
+def test_pool_sized_for_hbm_budget():
+    """K + V pools sized by BlockAllocator.blocks_for_budget for ~250 GB of fp16 Llama-3-8B
+    pages (32/8/128, 16-token pages: 64 KiB per page for K + V), capped by the free device
+    memory: the new tokens are appended through slot mappings built on the device at pages
+    in the top 1 % of the pool, then decode and prefill run there, against the oracle on the
+    compacted pages (the engine's sizing: engine_server.cpp:421,475-476)."""
+    torch.cuda.empty_cache()
+    free, _total = torch.cuda.mem_get_info()
+    budget = min(250 * 10**9, free - 12 * 10**9)
+    hkv, hq, d = 8, 32, 128
+    nb = kc.BlockAllocator.blocks_for_budget(budget, 16, hkv, d, torch.float16)
+    assert nb * 16 * hkv * d * 2 * 2 <= budget
+    say(f"pools sized for a {budget / 1e9:.0f} GB budget: {nb} pages "
+        f"({2 * nb * 16 * hkv * d * 2 / 1e9:.1f} GB of K + V)")
+    kp = torch.empty(nb, 16, hkv, d, dtype=torch.float16, device=DEV)
+    vp = torch.empty_like(kp)
+    g = torch.Generator().manual_seed(92)
+    lens = [700, 1, 333, 2048]
+    pages = [(L + 15) // 16 for L in lens]
+    top = nb - nb // 100   # the top 1 % of the pool
+    perm = torch.randperm(nb - top, generator=g)[: sum(pages)].to(torch.int32) + top
+    table, _ = wl._tables(lens, perm, max(pages))
+    used = perm.long().to(DEV)
+    kp.index_copy_(0, used, torch.randn(used.numel(), 16, hkv, d, generator=g).to(torch.float16).to(DEV))
+    vp.index_copy_(0, used, torch.randn(used.numel(), 16, hkv, d, generator=g).to(torch.float16).to(DEV))
+    B = len(lens)
+    td, ld = table.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV)
+    kn = torch.randn(B, hkv, d, generator=g).to(torch.float16).to(DEV)
+    vn = torch.randn(B, hkv, d, generator=g).to(torch.float16).to(DEV)
+    slots = kc.build_slots(td, torch.arange(B + 1, dtype=torch.int32, device=DEV), ld - 1, B)
+    kc.append_kv(kn, vn, slots, kp, vp)
+    q = torch.randn(B, hq, d, generator=g).to(torch.float16).to(DEV)
+    out = kc.paged_decode(q, kp, vp, td, ld, max(lens))
+    P = 32
+    qp = torch.randn(B * P, hq, d, generator=g).to(torch.float16).to(DEV)
+    cu = torch.tensor([0] + [min(P, L) for L in lens], dtype=torch.int32).cumsum(0).to(torch.int32)
+    qp = qp[: int(cu[-1])]
+    outp = kc.paged_prefill(qp, kp, vp, td, cu.to(DEV), ld, P, max(lens), causal=True)
+    torch.cuda.synchronize()
+    kh, vh, th = _compact_pages(kp, vp, table)
+    sl = slots.cpu().numpy()
+    kr = kh.reshape(-1, hkv, d)
+    for b in range(B):
+        pos = lens[b] - 1
+        assert sl[b] == int(table[b, pos // 16]) * 16 + pos % 16 and sl[b] >= top * 16
+        row = int(th[b, pos // 16]) * 16 + pos % 16
+        assert np.array_equal(kr[row], kn[b].float().cpu().numpy())
+    ref = oracle.paged_decode(q.float().cpu().numpy(), kh, vh, th.numpy(), np.array(lens), f64=True,
+                              nthreads=16)
+    check_lowp(out, ref, "decode, budget-sized pool", 2e-3, plain=True)
+    refp = oracle.paged_prefill(qp.float().cpu().numpy(), cu.numpy(), kh, vh, th.numpy(),
+                                np.array(lens, dtype=np.int32), True, f64=True, nthreads=16)
+    check_lowp(outp, refp, "prefill, budget-sized pool", 2e-3, plain=True)
+    del kp, vp
+    torch.cuda.empty_cache()
+
+
 def test_config5_mixed_step():
     """Configuration 5 at full size, one step: append (256 decode tokens + 4 x 1024 chunk
     tokens), decode of 256 lognormal contexts, then causal prefill of the chunks over a shared
@@ -835,9 +1002,9 @@ def test_config5_mixed_step():
     kd, vd, td = _compact_pages(kp, vp, dec.block_table)
     ref_d = oracle.paged_decode(dec.q.float().numpy(), kd, vd, td.numpy(), dec.seq_lens.numpy(),
                                 f64=True, nthreads=16)
-    check_lowp(out_d, ref_d, "cfg5 decode", 2e-3)
+    check_lowp(out_d, ref_d, "cfg5 decode", 2e-3, plain=True)
     del kd, vd
     kpp, vpp, tp = _compact_pages(kp, vp, pre.block_table)
     ref_p = oracle.paged_prefill(pre.q.float().numpy(), pre.cu_q.numpy(), kpp, vpp, tp.numpy(),
                                  pre.seq_lens.numpy(), True, f64=True, nthreads=16)
-    check_lowp(out_p, ref_p, "cfg5 prefill", 2e-3)
+    check_lowp(out_p, ref_p, "cfg5 prefill", 2e-3, plain=True)
