@@ -423,9 +423,11 @@ int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_ne
     if (!out || !q || !k_pool || !v_pool || !block_table || !seq_lens)
         return set_error(LLKV_ERR_INVALID, "%s: null pointer", fn);
     if (max_seq_len < 0) max_seq_len = 0;
-    if (max_seq_len > max_blocks_per_seq * block_size) max_seq_len = max_blocks_per_seq * block_size;
-    if ((int64_t)num_seqs * max_blocks_per_seq > INT32_MAX)
+    // token positions (max_blocks_per_seq * block_size) are int on the device
+    if ((int64_t)num_seqs * max_blocks_per_seq > INT32_MAX ||
+        (int64_t)max_blocks_per_seq * block_size > INT32_MAX)
         return set_error(LLKV_ERR_UNSUPPORTED, "%s: block table too large", fn);
+    if (max_seq_len > max_blocks_per_seq * block_size) max_seq_len = max_blocks_per_seq * block_size;
 
     const int G = num_q_heads / num_kv_heads;
     // The tuned bodies need 16-token pages, 16-byte aligned rows and pointers.

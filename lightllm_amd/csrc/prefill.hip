@@ -188,6 +188,10 @@ extern "C" int llkv_paged_prefill(void* out, const void* q, const void* k_pool,
     if (dtype_bytes(dtype) == 0) return set_error(LLKV_ERR_INVALID, "%s: unsupported dtype %d", fn, dtype);
     if (!out || !q || !k_pool || !v_pool || !block_table || !cu_q || !seq_lens)
         return set_error(LLKV_ERR_INVALID, "%s: null pointer", fn);
+    // token positions (max_blocks_per_seq * block_size) and table offsets are int on the device
+    if ((int64_t)max_blocks_per_seq * block_size > INT32_MAX ||
+        (int64_t)num_seqs * max_blocks_per_seq > INT32_MAX)
+        return set_error(LLKV_ERR_UNSUPPORTED, "%s: block table too large", fn);
     hipStream_t st = (hipStream_t)stream;
 
     MfmaPrefillArgs m = {};

@@ -98,6 +98,18 @@ def test_decode_rejects_small_workspace():
     assert rc == 3 and "workspace" in msg
 
 
+def test_table_position_overflow_rejected():
+    """max_blocks_per_seq * block_size must fit the kernels' int token positions."""
+    lib = L.lib()
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: the checks fail first
+    rc, msg = _err(lib.llkv_paged_decode(fake, fake, fake, fake, fake, fake, 1, 14, 2, 64, 16,
+                                         1 << 28, 4096, 0, 0.125, 0, fake, 1 << 20, None))
+    assert rc == 2 and "too large" in msg
+    rc, msg = _err(lib.llkv_paged_prefill(fake, fake, fake, fake, fake, 1 << 28, fake, fake, 1, 16,
+                                          16, 4096, 14, 2, 64, 16, 1, 0.125, 1, fake, 1 << 20, None))
+    assert rc == 2 and "too large" in msg
+
+
 def test_prefill_argument_checks():
     lib = L.lib()
     rc, msg = _err(lib.llkv_paged_prefill(None, None, None, None, None, 8, None, None, 1, 16, 16,
