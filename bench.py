@@ -25,9 +25,16 @@ Profiling helpers (the commands that produce the summaries under profiles/):
                                             CSV files (kernel trace, counters)
                                             found under DIR
   python bench.py --rocprof-traffic FETCH_DIR WRITE_DIR CAL_FETCH_DIR CAL_WRITE_DIR
-                                            HBM bytes per decode call from
-                                            FETCH_SIZE / WRITE_SIZE runs of this
-                                            benchmark and of --calibrate-copy
+                                            HBM bytes per call of the library's
+                                            kernels from FETCH_SIZE / WRITE_SIZE
+                                            runs of a --profile-target and of
+                                            --calibrate-copy
+  python bench.py --rocprof-mfma DIR        MFMA busy % of the prefill kernels from
+                                            an SQ_VALU_MFMA_BUSY_CYCLES +
+                                            GRBM_GUI_ACTIVE counter run
+  python bench.py --profile-target NAME     eager calls of one workload (cfg2_decode,
+                                            cfg3_decode, cfg5_decode, cfg4_prefill,
+                                            cfg5_prefill) for rocprofv3
 """
 from __future__ import annotations
 
@@ -52,14 +59,30 @@ METRIC = "paged decode µs/layer + achieved HBM GB/s (% peak) at B=64; prefill M
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it, with family / model / stepping (a virtualised
+    host may report a generic model name)."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" in line:
+                    k, v = line.split(":", 1)
+                    info.setdefault(k.strip(), v.strip())
+                if not line.strip() and info:
+                    break
     except OSError:
         pass
-    return platform.processor() or "unknown"
+    name = info.get("model name") or platform.processor() or "unknown"
+    extra = ", ".join(f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info)
+    return f"{name} ({extra})" if extra else name
+
+
+def cpu_threads() -> int:
+    """Host threads this process may use (the affinity mask; the GPU box gives a job 16)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
 
 
 def bench_decode(args, torch, kc, wl):
@@ -163,6 +186,7 @@ def bench_decode(args, torch, kc, wl):
         "case": case, "host_pools": (ke, ve), "step_ms": step_us / 1e3, "step_fused_us": fused_us,
         "decode_us_mean": dec_us, "decode_us_eager_median": statistics.median(eager_us),
         "decode_bytes": dec_bytes, "decode_bytes_pages": dec_bytes_pages, "append_bytes": app_bytes,
+        "pool_bytes": 2 * kps[0].numel() * kps[0].element_size(),
         "parity_ok": ok, "max_abs_err": float(err.max()),
     }
 
@@ -230,7 +254,9 @@ def bench_other_configs(torch, kc, wl):
         us = _graph_us(torch, lambda i: kc.paged_decode(q, pools[i % 2][0], pools[i % 2][1], bt, sl,
                                                        c3.max_seq_len, num_splits=S, out=out), 20)
         res[f"cfg3_decode_S{S}"] = {"us": round(us, 2),
-                                    "GBps": round(wl.decode_bytes(c3) / (us * 1e-6) / 1e9, 1)}
+                                    "GBps": round(wl.decode_bytes(c3) / (us * 1e-6) / 1e9, 1),
+                                    "GBps_page_granular": round(wl.decode_bytes(c3, exact_tokens=False)
+                                                                / (us * 1e-6) / 1e9, 1)}
     del pools
     m5 = wl.config5()
     dec, pre = m5.decode, m5.prefill
@@ -254,40 +280,13 @@ def bench_other_configs(torch, kc, wl):
     pf = wl.prefill_flops(pre)
     res["cfg5_step"] = {"us": round(step_us, 1), "decode_us": round(dec_us, 1),
                         "decode_GBps": round(wl.decode_bytes(dec) / (dec_us * 1e-6) / 1e9, 1),
+                        "decode_GBps_page_granular": round(wl.decode_bytes(dec, exact_tokens=False)
+                                                           / (dec_us * 1e-6) / 1e9, 1),
                         "prefill_us": round(pre_us, 1),
                         "prefill_mfma_frac": round(pf / (pre_us * 1e-6) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4)}
     res["rope_append_cfg5_step"] = bench_rope_append(torch, kc, dec, pre, kp, vp, dsl_slots, pslots)
     del kp, vp
     res["first_prefill_fp32_8x512"] = bench_first_prefill(torch, kc)
-    res.update(bench_head_dim_256(torch, kc, wl))
-    return res
-
-
-def bench_head_dim_256(torch, kc, wl):
-    """Gemma-2 head layout (16 q / 8 kv heads, head_dim 256), fp16: decode of 64 sequences with
-    contexts U[128, 2048] and prefill of 4 x 512 tokens on prefixes {0, 1024, 2048, 512}."""
-    dev = torch.device("cuda:0")
-    g = torch.Generator().manual_seed(5)
-    lens = torch.randint(128, 2049, (64,), generator=g).tolist()
-    need = sum((L + 1 + 15) // 16 for L in lens)
-    c = wl.decode_case("gemma2_decode", 64, 16, 8, 256, lens, need + 8, torch.float16, seed=3)
-    kp, vp = c.k_pool.to(dev), c.v_pool.to(dev)
-    q, bt, sl = c.q.to(dev), c.block_table.to(dev), c.seq_lens.to(dev)
-    out = torch.empty_like(q)
-    us = _graph_us(torch, lambda i: kc.paged_decode(q, kp, vp, bt, sl, c.max_seq_len, out=out), 20)
-    res = {"head_dim256_decode_fp16_B64": {"us": round(us, 1),
-                                           "GBps": round(wl.decode_bytes(c) / (us * 1e-6) / 1e9, 1)}}
-    del kp, vp
-    p = wl.prefill_case("gemma2_prefill", 16, 8, 256, [0, 1024, 2048, 512], [512] * 4, {}, 2048,
-                        torch.float16, 7)
-    kp, vp = p.k_pool.to(dev), p.v_pool.to(dev)
-    args = (p.q.to(dev), kp, vp, p.block_table.to(dev), p.cu_q.to(dev), p.seq_lens.to(dev),
-            p.max_q_len, p.max_seq_len, True)
-    out = torch.empty_like(args[0])
-    us = _graph_us(torch, lambda i: kc.paged_prefill(*args, out=out), 5)
-    tf = wl.prefill_flops(p) / (us * 1e-6) / 1e12
-    res["head_dim256_prefill_fp16"] = {"us": round(us, 1), "TFLOPs": round(tf, 1),
-                                       "mfma_frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4)}
     return res
 
 
@@ -386,7 +385,7 @@ def cpu_baseline(dec, budget_s: float):
         oracle.paged_decode(*args, nthreads=1)
         times.append(time.perf_counter() - t)
     med = statistics.median(times)
-    nthr = min(os.cpu_count() or 1, 64)
+    nthr = cpu_threads()
     tt = []
     for _ in range(5):
         t = time.perf_counter()
@@ -400,6 +399,60 @@ def cpu_baseline(dec, budget_s: float):
             "us_per_layer": round(med * 1e6, 1),
             "threads_all": {"threads": nthr, "us_per_layer": round(med_n * 1e6, 1),
                             "GB/s": round(dec["decode_bytes"] / med_n / 1e9, 3)},
+            "cpu_model": cpu_model(), "nproc": os.cpu_count()}
+
+
+def _time_cpu(fn, runs_min: int, budget_s: float):
+    fn()   # warm-up (page-in, thread start)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < runs_min or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline_prefill(torch, wl, budget_s: float):
+    """The oracle's paged prefill (the reference's cpu_prefill_attention_causal,
+    tests/test_paged_prefill.cu:164-210, restated in C) on configuration 4's whole batch:
+    1 thread (as the reference) and every thread of the host, median of >= 3 runs."""
+    import numpy as np
+    import oracle
+    c = wl.config4()
+    kp, vp = c.k_pool.float().numpy(), c.v_pool.float().numpy()
+    oracle.append_slots(kp, vp, c.k_chunk.float().numpy(), c.v_chunk.float().numpy(), c.slots.numpy())
+    args = (c.q.float().numpy(), c.cu_q.numpy(), kp, vp, c.block_table.numpy(), c.seq_lens.numpy(), True)
+    flops = wl.prefill_flops(c)
+    t1, n1 = _time_cpu(lambda: oracle.paged_prefill(*args, nthreads=1), 3, budget_s)
+    nthr = cpu_threads()
+    tn, nn = _time_cpu(lambda: oracle.paged_prefill(*args, nthreads=nthr), 3, budget_s / 3)
+    return {"value": round(flops / t1 / 1e9, 3), "unit": "GFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"configuration 4's whole batch (8 x 512 causal rows on cached prefixes, "
+                      f"14/2/64 fp16 widened to fp32), median of {n1} runs: {t1 * 1e6:.0f} us",
+            "us": round(t1 * 1e6, 1),
+            "threads_all": {"threads": nthr, "us": round(tn * 1e6, 1),
+                            "GFLOP/s": round(flops / tn / 1e9, 3), "runs": nn},
+            "cpu_model": cpu_model(), "nproc": os.cpu_count()}
+
+
+def cpu_baseline_decode_cfg3(torch, wl, budget_s: float):
+    """The oracle's decode (reconstruct_kv + cpu_attention) on configuration 3 (16 x 32768
+    tokens, fp16 K/V widened to fp32): 1 thread and every host thread."""
+    import oracle
+    c = wl.config3()
+    args = (c.q.float().numpy(), c.k_pool.float().numpy(), c.v_pool.float().numpy(),
+            c.block_table.numpy(), c.seq_lens.numpy())
+    nbytes = wl.decode_bytes(c)
+    t1, n1 = _time_cpu(lambda: oracle.paged_decode(*args, nthreads=1), 3, budget_s)
+    nthr = cpu_threads()
+    tn, nn = _time_cpu(lambda: oracle.paged_decode(*args, nthreads=nthr), 3, budget_s / 3)
+    return {"value": round(nbytes / t1 / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"configuration 3's whole batch (16 x 32768 tokens), median of {n1} runs: "
+                      f"{t1 * 1e6:.0f} us",
+            "us": round(t1 * 1e6, 1),
+            "threads_all": {"threads": nthr, "us": round(tn * 1e6, 1),
+                            "GB/s": round(nbytes / tn / 1e9, 3), "runs": nn},
             "cpu_model": cpu_model(), "nproc": os.cpu_count()}
 
 
@@ -417,6 +470,23 @@ def calibrate_copy(torch) -> None:
                       "bytes_written": COPY_CAL_BYTES, "launches": 5}))
 
 
+def _short_name(n: str) -> str:
+    """A kernel name without its argument list, demangled where rocprofv3 left it mangled."""
+    import re
+    import subprocess
+    if n.startswith("_Z"):
+        # binutils' c++filt predates the _Float16 mangling (DF16_); spell it as
+        # IEEE half (Dh) and rename afterwards
+        try:
+            d = subprocess.run(["c++filt", n.replace("DF16_", "Dh")], capture_output=True,
+                               text=True).stdout.strip()
+            n = d.replace("half", "_Float16") if d else n
+        except OSError:
+            pass
+    n = n.replace("(anonymous namespace)::", "")
+    return re.sub(r"\(.*", "", n).replace("void ", "").strip()[:100]
+
+
 def rocprof_summary(path: str) -> None:
     """Print per-kernel averages from rocprofv3 CSV output under `path`: kernel-trace
     durations (*kernel_trace.csv) and counter values (*counter_collection.csv)."""
@@ -425,23 +495,11 @@ def rocprof_summary(path: str) -> None:
     import re
     import subprocess
 
-    def short(n):
-        if n.startswith("_Z"):
-            # binutils' c++filt predates the _Float16 mangling (DF16_); spell it as
-            # IEEE half (Dh) and rename afterwards
-            try:
-                d = subprocess.run(["c++filt", n.replace("DF16_", "Dh")], capture_output=True,
-                                   text=True).stdout.strip()
-                n = d.replace("half", "_Float16") if d else n
-            except OSError:
-                pass
-        n = n.replace("(anonymous namespace)::", "")
-        return re.sub(r"\(.*", "", n).replace("void ", "").strip()[:100]
     for f in sorted(glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True)):
         agg = {}
         for r in csv.DictReader(open(f)):
             d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-            agg.setdefault(short(r["Kernel_Name"]), []).append(d)
+            agg.setdefault(_short_name(r["Kernel_Name"]), []).append(d)
         print(f"# kernel trace: {os.path.relpath(f, path)}")
         print(f"{'calls':>7} {'avg_us':>9} {'median_us':>9} {'min_us':>8} {'max_us':>8}  kernel")
         for n, ds in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
@@ -450,7 +508,7 @@ def rocprof_summary(path: str) -> None:
     for f in sorted(glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True)):
         agg = {}
         for r in csv.DictReader(open(f)):
-            key = (short(r["Kernel_Name"]), r["Counter_Name"])
+            key = (_short_name(r["Kernel_Name"]), r["Counter_Name"])
             agg.setdefault(key, []).append(float(r["Counter_Value"]))
         print(f"# counters: {os.path.relpath(f, path)}")
         print(f"{'dispatches':>10} {'mean_per_dispatch':>18}  counter  kernel")
@@ -468,16 +526,14 @@ def _counter_means(path: str, counter: str):
         for r in csv.DictReader(open(f)):
             if r["Counter_Name"] != counter:
                 continue
-            n = r["Kernel_Name"].replace("(anonymous namespace)::", "")
-            out.setdefault(re.sub(r"\(.*", "", n).replace("void ", "").strip(), []).append(
-                float(r["Counter_Value"]))
+            out.setdefault(_short_name(r["Kernel_Name"]), []).append(float(r["Counter_Value"]))
     return {k: statistics.fmean(v) for k, v in out.items()}
 
 
-def rocprof_traffic(fetch_dir, write_dir, cal_fetch_dir, cal_write_dir) -> None:
-    """Per-call HBM traffic of llkv_paged_decode on configuration 2: FETCH_SIZE and
-    WRITE_SIZE (KiB per dispatch) of its kernels, each scaled by bytes / counter of the
-    plain copy of --calibrate-copy."""
+def rocprof_traffic(fetch_dir, write_dir, cal_fetch_dir, cal_write_dir, match="llkv::") -> None:
+    """Per-call HBM traffic of the library's kernels in a --profile-target run: FETCH_SIZE
+    and WRITE_SIZE (KiB per dispatch) of each kernel whose name contains `match`, each
+    scaled by bytes / counter of the plain copy of --calibrate-copy."""
     cf = _counter_means(cal_fetch_dir, "FETCH_SIZE")
     cw = _counter_means(cal_write_dir, "WRITE_SIZE")
     copy_f = max((v for k, v in cf.items() if "copyBuffer" in k or "copy" in k.lower()), default=None)
@@ -491,15 +547,32 @@ def rocprof_traffic(fetch_dir, write_dir, cal_fetch_dir, cal_write_dir) -> None:
     print(f"scale: fetch {f_scale:.3f} B per unit, write {w_scale:.3f} B per unit")
     total = 0.0
     for k in sorted(set(fetch) | set(write)):
-        # configuration 2's plain decode: the fp32 split and merge kernels (not the
-        # fused-append instantiation the run also times)
-        if "decode" not in k or "float" not in k or "true" in k:
+        if match not in k or "copy_rows" in k:   # the workload's own kernels, not its set-up
             continue
         fb = fetch.get(k, 0.0) * f_scale
         wb = write.get(k, 0.0) * w_scale
         total += fb + wb
         print(f"{k}: read {fb / 1e6:.3f} MB, written {wb / 1e6:.3f} MB per dispatch")
     print(f"traffic_bytes_per_call: {total:.0f}")
+
+
+def rocprof_mfma(path: str, match="llkv::prefill_mfma", xcds: int = 8, simds: int = 1024) -> None:
+    """MFMA utilisation of the matching kernels from a counter run with SQ_VALU_MFMA_BUSY_CYCLES
+    and GRBM_GUI_ACTIVE: busy cycles / (active cycles of one XCD x SIMDs).  rocprofv3 sums
+    GRBM_GUI_ACTIVE over the XCDs, so one XCD's active cycles are that sum / xcds."""
+    busy = _counter_means(path, "SQ_VALU_MFMA_BUSY_CYCLES")
+    active = _counter_means(path, "GRBM_GUI_ACTIVE")
+    valu = _counter_means(path, "SQ_INSTS_VALU")
+    mfma = _counter_means(path, "SQ_INSTS_MFMA")
+    for k in sorted(busy):
+        if match not in k:
+            continue
+        cyc = active.get(k, 0.0) / xcds
+        util = busy[k] / (cyc * simds) if cyc else 0.0
+        print(f"{k}: SQ_VALU_MFMA_BUSY_CYCLES {busy[k]:.0f}, GRBM_GUI_ACTIVE {active.get(k, 0):.0f} "
+              f"({cyc:.0f} per XCD), MFMA busy {100 * util:.1f} % of {simds} SIMDs; "
+              f"SQ_INSTS_MFMA {mfma.get(k, 0):.0f}, SQ_INSTS_VALU {valu.get(k, 0):.0f} "
+              f"(VALU / MFMA instructions {valu.get(k, 0) / max(mfma.get(k, 1), 1):.2f})")
 
 
 def read_traffic():
@@ -516,6 +589,62 @@ def read_traffic():
     return None
 
 
+def profile_target(torch, kc, wl, name: str, iters: int) -> None:
+    """Eager launches of one workload for rocprofv3 (kernel trace or counters): warm-up, then
+    `iters` calls, each on the workload's own inputs.  Prints one line naming what ran."""
+    dev = torch.device("cuda:0")
+    if name in ("cfg2_decode", "cfg3_decode"):
+        case = wl.config2() if name == "cfg2_decode" else wl.config3()
+        B, hq, d = case.q.shape
+        hkv, nb = case.k_pool.shape[2], case.k_pool.shape[0]
+        layers = 8 if name == "cfg2_decode" else 2
+        pools = [wl.device_pools(nb, hkv, d, case.k_pool.dtype, 100 + i, dev) for i in range(layers)]
+        q, bt, sl = case.q.to(dev), case.block_table.to(dev), case.seq_lens.to(dev)
+        out = torch.empty_like(q)
+        ml = case.max_seq_len
+        ws = kc._workspace(kc.decode_workspace_bytes(B, hq, hkv, d, 16, ml), dev)
+        fn = lambda i: kc.paged_decode(q, pools[i % layers][0], pools[i % layers][1], bt, sl, ml,
+                                       out=out, workspace=ws)
+        what = f"{name}: llkv_paged_decode, {layers} layer pools rotated, {wl.decode_bytes(case)} B per call"
+    elif name in ("cfg5_decode", "cfg5_prefill"):
+        m5 = wl.config5()
+        kp, vp = wl.device_pools(262144, 8, 128, torch.float16, 55, dev)
+        if name == "cfg5_decode":
+            c = m5.decode
+            q, bt, sl = c.q.to(dev), c.block_table.to(dev), c.seq_lens.to(dev)
+            out = torch.empty_like(q)
+            fn = lambda i: kc.paged_decode(q, kp, vp, bt, sl, c.max_seq_len, out=out)
+            what = f"{name}: llkv_paged_decode, {wl.decode_bytes(c)} B per call"
+        else:
+            c = m5.prefill
+            kc.append_kv(c.k_chunk.to(dev), c.v_chunk.to(dev), c.slots.to(dev), kp, vp)
+            q, bt, cu, sl = c.q.to(dev), c.block_table.to(dev), c.cu_q.to(dev), c.seq_lens.to(dev)
+            out = torch.empty_like(q)
+            fn = lambda i: kc.paged_prefill(q, kp, vp, bt, cu, sl, c.max_q_len, c.max_seq_len, True,
+                                            out=out)
+            what = f"{name}: llkv_paged_prefill, {wl.prefill_flops(c)} FLOP per call"
+    elif name == "cfg4_prefill":
+        c = wl.config4()
+        kp, vp = c.k_pool.to(dev), c.v_pool.to(dev)
+        kc.append_kv(c.k_chunk.to(dev), c.v_chunk.to(dev), c.slots.to(dev), kp, vp)
+        q, bt, cu, sl = c.q.to(dev), c.block_table.to(dev), c.cu_q.to(dev), c.seq_lens.to(dev)
+        out = torch.empty_like(q)
+        fn = lambda i: kc.paged_prefill(q, kp, vp, bt, cu, sl, c.max_q_len, c.max_seq_len, True, out=out)
+        what = f"{name}: llkv_paged_prefill, {wl.prefill_flops(c)} FLOP per call"
+    else:
+        raise SystemExit(f"unknown profile target {name}")
+    for i in range(3):
+        fn(i)
+    torch.cuda.synchronize()
+    for i in range(iters):
+        fn(i)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_target": what, "calls": iters}), flush=True)
+
+
+PROFILE_TARGETS = ("cfg2_decode", "cfg3_decode", "cfg5_decode", "cfg4_prefill", "cfg5_prefill")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -529,12 +658,19 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--rocprof-summary", metavar="DIR")
     ap.add_argument("--rocprof-traffic", nargs=4, metavar="DIR")
+    ap.add_argument("--rocprof-mfma", metavar="DIR")
+    ap.add_argument("--profile-target", choices=PROFILE_TARGETS,
+                    help="eager launches of one workload for rocprofv3, no JSON line")
+    ap.add_argument("--profile-iters", type=int, default=20)
     args = ap.parse_args()
     if args.rocprof_summary:
         rocprof_summary(args.rocprof_summary)
         return
     if args.rocprof_traffic:
         rocprof_traffic(*args.rocprof_traffic)
+        return
+    if args.rocprof_mfma:
+        rocprof_mfma(args.rocprof_mfma)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build's path has no multi-GPU "
@@ -547,6 +683,9 @@ def main():
         return
     from lightllm_amd import kv_cache as kc
     from lightllm_amd import workloads as wl
+    if args.profile_target:
+        profile_target(torch, kc, wl, args.profile_target, args.profile_iters)
+        return
 
     dec = bench_decode(args, torch, kc, wl)
     pre = None if args.no_prefill else bench_prefill(args, torch, kc, wl)
@@ -572,7 +711,9 @@ def main():
         "data": "synthetic (seeded N(0,1) K/V/Q, random page permutation)",
         "config": {"workload": "cfg2: paged decode + KV append, B=64, Hq=14 Hkv=2 D=64 fp32, "
                                "L~U[128,2048]+1, pool 32768 x 16-token pages",
-                   "batch": 64, "layers_rotated": args.layers},
+                   "batch": 64, "layers_rotated": args.layers,
+                   "pool_bytes_per_layer": dec["pool_bytes"],
+                   "touched_bytes_per_rotation": dec["decode_bytes_pages"] * args.layers},
         "us_per_layer": round(step_us, 2),
         "step_GBps_incl_append": round(step_gbs, 1),
         "us_per_layer_fused_append": round(dec["step_fused_us"], 2),
@@ -586,17 +727,24 @@ def main():
                                "decode_merge_kernel<float,1>)",
                      "bytes_per_launch": dec["decode_bytes"],
                      "timing": "HIP events on the launch stream around a HIP-graph replay of "
-                               "--steps llkv_paged_decode calls (4 layer pools rotated)"},
+                               f"--steps llkv_paged_decode calls ({args.layers} layer pools rotated, "
+                               "so a rotation touches more than twice the 256 MB last-level cache)"},
         "parity_ok": dec["parity_ok"],
         "cpu_baseline": cpu,
     }
     if pre is not None:
         line["prefill_cfg4"] = {"us": round(pre["us"], 2), "TFLOPs": round(pre["tflops"], 1),
-                                "mfma_frac": round(pre["mfma_frac"], 4), "flop": pre["flop"]}
+                                "mfma_frac": round(pre["mfma_frac"], 4), "flop": pre["flop"],
+                                "note": "HIP-graph replays of one call on the same 6.2 MB of K/V "
+                                        "(MFMA-bound: its inputs stay cache-resident)",
+                                "cpu_baseline": None if args.no_cpu_baseline else
+                                cpu_baseline_prefill(torch, wl, args.cpu_budget)}
         pre32 = bench_prefill(args, torch, kc, wl, dtype=torch.float32)
         line["prefill_cfg4_shape_fp32"] = {"us": round(pre32["us"], 2), "TFLOPs": round(pre32["tflops"], 1),
                                            "mfma_frac_of_fp32_peak": round(pre32["mfma_frac"], 4)}
     if other is not None:
+        if not args.no_cpu_baseline:
+            other["cfg3_decode_S0"]["cpu_baseline"] = cpu_baseline_decode_cfg3(torch, wl, args.cpu_budget)
         line["other_configs"] = other
     print(json.dumps(line), flush=True)
 
