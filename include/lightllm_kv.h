@@ -178,6 +178,23 @@ int llkv_paged_decode(void* out, const void* q, const void* k_pool,
                       float scale, int dtype, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* Paged decode that allocates nothing and takes no workspace: llkv_paged_decode
+ * with its split partials in a device array of the library
+ * (llkv_paged_decode_noalloc_max_bytes() = 16 MiB per GPU, held until the
+ * process ends).  No counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops).
+ * Shapes whose llkv_paged_decode_workspace_size() exceeds the array are
+ * rejected with LLKV_ERR_WORKSPACE.  Calls that overlap on one GPU share the
+ * array and race: order them on one stream.  Results are those of
+ * llkv_paged_decode with the same arguments. */
+size_t llkv_paged_decode_noalloc_max_bytes(void);
+int llkv_paged_decode_noalloc(void* out, const void* q, const void* k_pool,
+                              const void* v_pool, const int* block_table,
+                              const int* seq_lens, int num_seqs, int num_q_heads,
+                              int num_kv_heads, int head_dim, int block_size,
+                              int max_blocks_per_seq, int max_seq_len, int num_splits,
+                              float scale, int dtype, void* stream);
+
 /* Fused KV append + paged decode: llkv_append of the step's new rows followed
  * by llkv_paged_decode, in one launch (plus the merge).  Replaces a
  * paged_attention call (src/engine/engine_server.cpp:1812-1817) together with

@@ -47,6 +47,10 @@ _SIGS = {
     "llkv_paged_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                   c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int,
                                   c_void_p, c_size_t, c_void_p]),
+    "llkv_paged_decode_noalloc_max_bytes": (c_size_t, []),
+    "llkv_paged_decode_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                          c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                          c_float, c_int, c_void_p]),
     "llkv_paged_decode_append": (c_int, [c_void_p] * 8 + [c_int] * 8 + [c_float, c_int, c_void_p,
                                                                          c_size_t, c_void_p]),
     "llkv_paged_prefill_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int,

@@ -551,3 +551,60 @@ extern "C" int llkv_paged_decode_append(void* out, const void* q, const void* k_
                              max_blocks_per_seq, max_seq_len, num_splits, scale, dtype, workspace,
                              workspace_bytes, stream);
 }
+
+// ---------------------------------------------------------------------------
+// Decode without a caller workspace: the split partials go to a file-scope
+// device array (kNoAllocScratchBytes per GPU, held until the process ends),
+// for callers that cannot allocate.  Its device address is looked up once per
+// device (hipGetSymbolAddress) and kept; kernels receive that address, never
+// the array's host-side name.  The decode kernels write every partial before
+// reading it within a call, so nothing needs clearing; calls that overlap on
+// one GPU share the array and race.
+// ---------------------------------------------------------------------------
+namespace llkv {
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = 16u << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+int scratch_address(const char* fn, void** out) {
+    static std::mutex mu;
+    static void* ptrs[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return set_error(LLKV_ERR_HIP, "%s: no current device", fn);
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptrs[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return set_error(LLKV_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", fn,
+                             hipGetErrorString(e));
+        ptrs[dev] = p;
+    }
+    *out = ptrs[dev];
+    return LLKV_OK;
+}
+
+}  // namespace
+}  // namespace llkv
+
+extern "C" size_t llkv_paged_decode_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int llkv_paged_decode_noalloc(void* out, const void* q, const void* k_pool,
+                                         const void* v_pool, const int* block_table,
+                                         const int* seq_lens, int num_seqs, int num_q_heads,
+                                         int num_kv_heads, int head_dim, int block_size,
+                                         int max_blocks_per_seq, int max_seq_len, int num_splits,
+                                         float scale, int dtype, void* stream) {
+    // (the schedule chosen for this call decides the bytes it needs; a shape
+    // beyond the array fails the impl's workspace check with LLKV_ERR_WORKSPACE)
+    const char* fn = "llkv_paged_decode_noalloc (16 MiB device scratch array)";
+    if (num_seqs == 0) return LLKV_OK;
+    void* ws = nullptr;
+    if (int e = scratch_address(fn, &ws)) return e;
+    return paged_decode_impl(fn, out, q, nullptr, nullptr, k_pool, v_pool, block_table, seq_lens,
+                             num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                             max_blocks_per_seq, max_seq_len, num_splits, scale, dtype, ws,
+                             kNoAllocScratchBytes, stream);
+}
