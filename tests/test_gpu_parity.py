@@ -608,6 +608,13 @@ PREFILL = [
     ("bf16_D96_long", 8, 8, 96, [2300, 10], [70, 129], torch.bfloat16, True),
     ("fp32_D96", 8, 4, 96, [40, 700], [33, 150], torch.float32, True),
     ("fp32_D96_long_noncausal", 4, 4, 96, [2200], [60], torch.float32, False),
+    # the shapes of the reference's tests/test_paged_prefill.cu sections 1-3 and 5 (:342-740):
+    # one token over 24 keys; 4 tokens over the same 32 keys; 4 new tokens on a 16-token
+    # history; 32 tokens over the same 256 keys
+    ("ref_s1_single_token", 4, 2, 64, [23], [1], torch.float32, True),
+    ("ref_s2_multi_token", 4, 2, 64, [28], [4], torch.float32, False),
+    ("ref_s3_chunked", 4, 2, 64, [16], [4], torch.float32, True),
+    ("ref_s5_stress", 4, 2, 64, [224], [32], torch.float32, False),
 ]
 
 
