@@ -167,6 +167,12 @@ __device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* orde
 #ifndef LLKV_PREFILL_INTERLEAVE
 #define LLKV_PREFILL_INTERLEAVE 1
 #endif
+#ifndef LLKV_PF_VTR
+#define LLKV_PF_VTR 1
+#endif
+#ifndef LLKV_PF_DMA
+#define LLKV_PF_DMA 1
+#endif
 
 constexpr int kPageWindow = 256;   // page ids staged in LDS at a time
 
@@ -249,9 +255,26 @@ __device__ inline void poison_uncovered_rows(const MfmaPrefillArgs& a, const Wor
     }
 }
 
-template <int D>
+// Direct-to-LDS load of 16 bytes per lane: lane L's bytes land at LDS address
+// lds + 16 L (lds uniform over the wave).  Issued as inline assembly, so that
+// the compiler, which cannot tell the two tile buffers apart, does not wait for
+// it before every LDS read of the other buffer; the caller waits (vmcnt) before
+// the barrier that publishes the tile.  A later load only lengthens the
+// compiler's own in-order vmcnt waits.
+__device__ inline void dma16(const void* gptr, const void* lds) {
+    const uint32_t la = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gptr), "s"(la)
+                 : "memory", "m0");
+}
+
+// DMA: K/V tiles written by direct-to-LDS loads in 1 KB blocks, so rows are
+// unpadded and their 16-byte chunks XOR-swizzled by row instead.
+template <int D, bool DMA>
 struct Smem {
-    static constexpr int KPAD = D + 8;    // halves per K row (pad: spread LDS banks)
+    static constexpr int KPAD = DMA ? D : D + 8;   // halves per K row (pad: spread LDS banks)
     static constexpr int VPAD = BN + 8;   // halves per V^T row
     union {
         struct {
@@ -268,14 +291,21 @@ struct Smem {
 // page table.
 template <typename T, int D, bool CG>
 __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
-    constexpr int KPAD = Smem<D>::KPAD, VPAD = Smem<D>::VPAD;
+    // Direct-to-LDS staging (head_dim 64 / 128): wave w loads page w of the
+    // tile (rows 16w .. 16w + 15) of K and of V, RPB rows per 1 KB block.
+    constexpr bool kDma = LLKV_PF_DMA && LLKV_PF_VTR && (D == 64 || D == 128);
+    using SM = Smem<D, kDma>;
+    constexpr int KPAD = SM::KPAD, VPAD = SM::VPAD;
+    constexpr int CPR = D / 8;            // 16-byte chunks per row
+    constexpr int RPB = 64 / CPR;         // rows per 1 KB block
+    constexpr int BPW = 16 / RPB;         // blocks per wave (one page) per tile
     constexpr int KS = D / 32;            // k-steps of the QK^T product
     constexpr int DT = D / 16;            // 16-dim tiles of the output
     constexpr int KCH = BN * D / 8;       // 16-byte K chunks per tile
     constexpr int KCH_T = KCH / 256;      // per thread
     constexpr int VT_N = (BN / 2) * (D / 8);          // V tasks (2 keys x 8 dims) per tile
     constexpr int VT_T = (VT_N + 255) / 256;          // per thread (head_dim 96: the last partly idle)
-    __shared__ Smem<D> sm;
+    __shared__ SM sm;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -339,7 +369,16 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     // ---- staging: global -> registers -> LDS -----------------------------
     int tbase = 0;   // first page id held in sm.pages
     u32x4 kr[KCH_T];
-    u32x4 vr[VT_T][2];
+#if LLKV_PF_VTR
+    // V is staged like K (row-major, K's row stride) and read transposed by
+    // ds_read_b64_tr_b16; its rows share K's page addresses.
+    using VReg = u32x4[KCH_T];
+#else
+    using VReg = u32x4[VT_T][2];
+#endif
+    VReg vr;
+    static_assert(!LLKV_PF_VTR || D * VPAD >= BN * KPAD, "row-major V tile fits the V^T buffer");
+    static_assert(KCH % 256 == 0, "K chunks spread evenly over the threads");
     // Per-thread byte offsets inside a page and page slot of each staged row;
     // a load is then base + phys * page_bytes + offset (one 32x32->64 multiply-add).
     // Contiguous K/V: the key within the tile and the byte offset in the row.
@@ -347,8 +386,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const uint32_t page_bytes = row_bytes * kPage;
     const char* kb = reinterpret_cast<const char*>(kg);
     const char* vb = reinterpret_cast<const char*>(vg);
-    uint32_t koff[KCH_T], voff[VT_T];
-    int kslot[KCH_T], vslot[VT_T];
+    uint32_t koff[KCH_T];
+    int kslot[KCH_T];
 #pragma unroll
     for (int j = 0; j < KCH_T; ++j) {
         const int ch = tid + 256 * j;
@@ -356,6 +395,9 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         kslot[j] = CG ? key : key >> 4;
         koff[j] = (CG ? 0u : (uint32_t)(key & 15) * row_bytes) + (uint32_t)c * 16u;
     }
+#if !LLKV_PF_VTR
+    uint32_t voff[VT_T];
+    int vslot[VT_T];
 #pragma unroll
     for (int j = 0; j < VT_T; ++j) {
         const int task = (VT_N % 256 == 0 || tid + 256 * j < VT_N) ? tid + 256 * j : 0;   // idle: task 0's rows
@@ -363,13 +405,19 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         vslot[j] = CG ? 2 * kp : (2 * kp) >> 4;
         voff[j] = (CG ? 0u : (uint32_t)((2 * kp) & 15) * row_bytes) + (uint32_t)c * 16u;
     }
-    auto load_tile = [&](int t, u32x4 (&kreg)[KCH_T], u32x4 (&vreg)[VT_T][2]) {
+#endif
+    auto load_tile = [&](int t, u32x4 (&kreg)[KCH_T], VReg& vreg) {
         if constexpr (CG) {   // rows past the sequence's last are staged as the last
             const int key0 = t * BN, last = L - 1;
 #pragma unroll
-            for (int j = 0; j < KCH_T; ++j)
-                kreg[j] = *reinterpret_cast<const u32x4*>(
-                    kb + (uint64_t)min(key0 + kslot[j], last) * row_bytes + koff[j]);
+            for (int j = 0; j < KCH_T; ++j) {
+                const uint64_t off = (uint64_t)min(key0 + kslot[j], last) * row_bytes + koff[j];
+                kreg[j] = *reinterpret_cast<const u32x4*>(kb + off);
+#if LLKV_PF_VTR
+                vreg[j] = *reinterpret_cast<const u32x4*>(vb + off);
+#endif
+            }
+#if !LLKV_PF_VTR
 #pragma unroll
             for (int j = 0; j < VT_T; ++j) {
                 vreg[j][0] = *reinterpret_cast<const u32x4*>(
@@ -377,15 +425,20 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 vreg[j][1] = *reinterpret_cast<const u32x4*>(
                     vb + (uint64_t)min(key0 + vslot[j] + 1, last) * row_bytes + voff[j]);
             }
+#endif
             return;
         }
         // pages past the sequence's last are staged as the last page (valid memory)
         const int* pg = sm.pages + (4 * t - tbase);
 #pragma unroll
         for (int j = 0; j < KCH_T; ++j) {
-            const uint64_t phys = (uint32_t)max(pg[kslot[j]], 0);
-            kreg[j] = *reinterpret_cast<const u32x4*>(kb + phys * page_bytes + koff[j]);
+            const uint64_t off = (uint64_t)(uint32_t)max(pg[kslot[j]], 0) * page_bytes + koff[j];
+            kreg[j] = *reinterpret_cast<const u32x4*>(kb + off);
+#if LLKV_PF_VTR
+            vreg[j] = *reinterpret_cast<const u32x4*>(vb + off);
+#endif
         }
+#if !LLKV_PF_VTR
 #pragma unroll
         for (int j = 0; j < VT_T; ++j) {
             const uint64_t phys = (uint32_t)max(pg[vslot[j]], 0);
@@ -393,14 +446,19 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             vreg[j][0] = *reinterpret_cast<const u32x4*>(p);
             vreg[j][1] = *reinterpret_cast<const u32x4*>(p + row_bytes);
         }
+#endif
     };
-    auto store_tile = [&](int buf, const u32x4 (&kreg)[KCH_T], const u32x4 (&vreg)[VT_T][2]) {
+    auto store_tile = [&](int buf, const u32x4 (&kreg)[KCH_T], const VReg& vreg) {
 #pragma unroll
         for (int j = 0; j < KCH_T; ++j) {
             const int ch = tid + 256 * j;
             const int key = ch / (D / 8), c = ch % (D / 8);
             *reinterpret_cast<u32x4*>(&sm.k[buf][key * KPAD + c * 8]) = kreg[j];
+#if LLKV_PF_VTR
+            *reinterpret_cast<u32x4*>(&sm.vt[buf][key * KPAD + c * 8]) = vreg[j];
+#endif
         }
+#if !LLKV_PF_VTR
 #pragma unroll
         for (int j = 0; j < VT_T; ++j) {
             const int task = tid + 256 * j;
@@ -417,7 +475,37 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 dst[(2 * e2 + 1) * (VPAD / 2)] = __builtin_amdgcn_perm(a1[e2], a0[e2], 0x07060302u);
             }
         }
+#endif
     };
+    // Half-column hc of tile row `row` in LDS: with DMA the 16-byte chunk
+    // index is XOR-ed with the row (mod the chunks per row).
+    auto scol = [&](int row, int hc) {
+        if constexpr (kDma) return (((hc >> 3) ^ (row & (CPR - 1))) << 3) | (hc & 7);
+        return hc;
+    };
+    // A operand of O^T = V^T P^T for output dims dt*16 .. +15 and the 32-key
+    // half ss: lane (g, c16) holds dim dt*16 + c16 of keys 32 ss + 8 g .. + 7.
+#if LLKV_PF_VTR
+    // ds_read_b64_tr_b16 within each 16-lane group: output lane 4a + e gets
+    // element e of the 4 halves addressed by lanes a, a + 4, a + 8, a + 12; so
+    // lane c16 addresses row (key) c16 / 4, dims 4 (c16 % 4) .. + 3, and each
+    // lane receives its dim over 4 consecutive keys (two reads: 8 keys).
+    auto v_operand = [&](int buf, int dt, int ss) {
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        const int r0 = 32 * ss + 8 * g + (c16 >> 2), hc = dt * 16 + 4 * (c16 & 3);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(&sm.vt[buf][r0 * KPAD + scol(r0, hc)]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(&sm.vt[buf][(r0 + 4) * KPAD + scol(r0 + 4, hc)]));
+        typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+        const u32x2v l2 = __builtin_bit_cast(u32x2v, lo), h2 = __builtin_bit_cast(u32x2v, hi);
+        return make_uint4(l2.x, l2.y, h2.x, h2.y);
+    };
+#else
+    auto v_operand = [&](int buf, int dt, int ss) {
+        return *reinterpret_cast<const uint4*>(&sm.vt[buf][(dt * 16 + c16) * VPAD + 32 * ss + 8 * g]);
+    };
+#endif
 
     // Page ids live in LDS so that no K/V load waits behind a table load.
     auto stage_pages = [&](int base) {
@@ -426,11 +514,50 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         for (int i = tid; i < kPageWindow; i += 256) sm.pages[i] = bt[min(base + i, last_page)];
         lds_barrier();   // the page ids are in LDS; no global load needs to have landed
     };
+    // Direct-to-LDS: lane L of block j writes LDS chunk L of rows 16w + j RPB ..,
+    // i.e. row 16w + j RPB + L / CPR, chunk position L % CPR, which holds the
+    // row's global chunk (L % CPR) ^ (row % CPR).
+    uint32_t dma_off[BPW];   // byte offset of the lane's chunk inside its page (paged) / row (CG)
+    int dma_row[BPW];        // the lane's row within the wave's page
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        const int r = j * RPB + lane / CPR;
+        const int c = (lane % CPR) ^ (r % CPR);
+        dma_row[j] = r;
+        dma_off[j] = (CG ? 0u : (uint32_t)r * row_bytes) + (uint32_t)c * 16u;
+    }
+    auto dma_tile = [&](int t, int buf) {
+        if constexpr (kDma) {
+            uint64_t base;   // byte offset of the wave's page (paged) or of the tile's first row (CG)
+            if constexpr (!CG) {
+                const int phys = __builtin_amdgcn_readfirstlane(max(sm.pages[4 * t + w - tbase], 0));
+                base = (uint64_t)(uint32_t)phys * page_bytes;
+            }
+#pragma unroll
+            for (int j = 0; j < BPW; ++j) {
+                uint64_t off;
+                if constexpr (CG) {   // rows past the sequence's last are staged as the last
+                    const int key = min(t * BN + 16 * w + dma_row[j], L - 1);
+                    off = (uint64_t)key * row_bytes + dma_off[j];
+                } else {
+                    off = base + dma_off[j];
+                }
+                const int lrow = 16 * w + j * RPB;
+                dma16(kb + off, &sm.k[buf][lrow * KPAD]);
+                dma16(vb + off, &sm.vt[buf][lrow * KPAD]);
+            }
+        }
+    };
     if (t_begin < t_end) {
         stage_pages(4 * t_begin);
         load_q();
-        load_tile(t_begin, kr, vr);
-        store_tile(0, kr, vr);
+        if constexpr (kDma) {
+            dma_tile(t_begin, 0);
+            __builtin_amdgcn_s_waitcnt(0x3F70);   // vmcnt(0): this wave's blocks are in LDS
+        } else {
+            load_tile(t_begin, kr, vr);
+            store_tile(0, kr, vr);
+        }
     }
     __syncthreads();
 
@@ -440,7 +567,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             // tile t+1 covers pages [4(t+1), 4(t+1)+4); restage when they leave the window
             // (uniform branch; every earlier read of sm.pages preceded the last barrier)
             if (4 * (t + 1) + 4 > tbase + kPageWindow) stage_pages(4 * (t + 1));
-            load_tile(t + 1, kr, vr);
+            if constexpr (kDma) dma_tile(t + 1, buf ^ 1);
+            else load_tile(t + 1, kr, vr);
         }
         __builtin_amdgcn_sched_barrier(0);   // next tile's loads issue before this tile's MFMAs
         LLKV_PF_PRIO(LLKV_PF_SETPRIO >= 1 && D >= 128, 1);
@@ -457,7 +585,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const uint4 ka =
-                    *reinterpret_cast<const uint4*>(&sm.k[buf][krow * KPAD + ks * 32 + g * 8]);
+                    *reinterpret_cast<const uint4*>(&sm.k[buf][krow * KPAD + scol(krow, ks * 32 + g * 8)]);
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) s[kt][nt] = Mfma<T>::mma(ka, qop[nt][ks], s[kt][nt]);
             }
@@ -543,7 +671,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
             uint4 va0[DT], va1[DT];
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
-                va0[dt] = *reinterpret_cast<const uint4*>(&sm.vt[buf][(dt * 16 + c16) * VPAD + 8 * g]);
+                va0[dt] = v_operand(buf, dt, 0);
             float pv1[2][2][4];   // [query tile][h][i] of the second half
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -552,8 +680,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
                     const int dt = k >> 1, nt = k & 1;
                     o[dt][nt] = Mfma<T>::mma(va0[dt], pop[0][nt], o[dt][nt]);
                     if (nt == 1)
-                        va1[dt] = *reinterpret_cast<const uint4*>(
-                            &sm.vt[buf][(dt * 16 + c16) * VPAD + 32 + 8 * g]);
+                        va1[dt] = v_operand(buf, dt, 1);
                 } else {
                     const int nt = k - 2 * DT;
                     osum[nt] = Mfma<T>::mma(ones, pop[0][nt], osum[nt]);
@@ -583,8 +710,7 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
         auto pv_half = [&](int ss) {
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                const uint4 va = *reinterpret_cast<const uint4*>(
-                    &sm.vt[buf][(dt * 16 + c16) * VPAD + 32 * ss + 8 * g]);
+                const uint4 va = v_operand(buf, dt, ss);
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) o[dt][nt] = Mfma<T>::mma(va, pop[ss][nt], o[dt][nt]);
             }
@@ -598,7 +724,11 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
 #endif
 
         LLKV_PF_PRIO(LLKV_PF_SETPRIO >= 2 && D >= 128, 0);
-        if (t + 1 < t_end) store_tile(buf ^ 1, kr, vr);
+        if constexpr (kDma) {
+            if (t + 1 < t_end) __builtin_amdgcn_s_waitcnt(0x3F70);   // vmcnt(0): tile t+1 in LDS
+        } else {
+            if (t + 1 < t_end) store_tile(buf ^ 1, kr, vr);
+        }
         __syncthreads();
     }
 
