@@ -289,8 +289,10 @@ struct Smem {
 // CG: contiguous K/V (first prefill): key j of the sequence is row kvo + j of
 // k / v; the staged rows are clamped to the sequence's last, and there is no
 // page table.
+// head_dim 128: two waves per SIMD (<= 256 registers).
 template <typename T, int D, bool CG>
-__global__ __launch_bounds__(256) void prefill_mfma_kernel(MfmaPrefillArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 1)))
+void prefill_mfma_kernel(MfmaPrefillArgs a) {
     // Direct-to-LDS staging (head_dim 64 / 128): wave w loads page w of the
     // tile (rows 16w .. 16w + 15) of K and of V, RPB rows per 1 KB block.
     constexpr bool kDma = LLKV_PF_DMA && LLKV_PF_VTR && (D == 64 || D == 128);
