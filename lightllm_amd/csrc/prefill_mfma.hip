@@ -301,6 +301,9 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
     constexpr int CPR = D / 8;            // 16-byte chunks per row
     constexpr int RPB = 64 / CPR;         // rows per 1 KB block
     constexpr int BPW = 16 / RPB;         // blocks per wave (one page) per tile
+    // Chunk swizzle of tile row r: row bits 0, 1, 3, 4 (the QK^T operand reads
+    // rows 8 (c16 / 4) + 4 h + c16 % 4 together, so rows 8 apart must differ).
+    auto swz_row = [](int r) { return ((r & 3) | ((r >> 1) & 0xC)) & (CPR - 1); };
     constexpr int KS = D / 32;            // k-steps of the QK^T product
     constexpr int DT = D / 16;            // 16-dim tiles of the output
     constexpr int KCH = BN * D / 8;       // 16-byte K chunks per tile
@@ -482,7 +485,7 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
     // Half-column hc of tile row `row` in LDS: with DMA the 16-byte chunk
     // index is XOR-ed with the row (mod the chunks per row).
     auto scol = [&](int row, int hc) {
-        if constexpr (kDma) return (((hc >> 3) ^ (row & (CPR - 1))) << 3) | (hc & 7);
+        if constexpr (kDma) return (((hc >> 3) ^ swz_row(row)) << 3) | (hc & 7);
         return hc;
     };
     // A operand of O^T = V^T P^T for output dims dt*16 .. +15 and the 32-key
@@ -518,13 +521,13 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
     };
     // Direct-to-LDS: lane L of block j writes LDS chunk L of rows 16w + j RPB ..,
     // i.e. row 16w + j RPB + L / CPR, chunk position L % CPR, which holds the
-    // row's global chunk (L % CPR) ^ (row % CPR).
+    // row's global chunk (L % CPR) ^ swz_row(row).
     uint32_t dma_off[BPW];   // byte offset of the lane's chunk inside its page (paged) / row (CG)
     int dma_row[BPW];        // the lane's row within the wave's page
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
         const int r = j * RPB + lane / CPR;
-        const int c = (lane % CPR) ^ (r % CPR);
+        const int c = (lane % CPR) ^ swz_row(16 * w + r);
         dma_row[j] = r;
         dma_off[j] = (CG ? 0u : (uint32_t)r * row_bytes) + (uint32_t)c * 16u;
     }
