@@ -270,6 +270,21 @@ __device__ inline void dma16(const void* gptr, const void* lds) {
                  : "memory", "m0");
 }
 
+// The same with a wave-uniform base (scalar registers) and a 32-bit per-lane
+// byte offset (no per-lane 64-bit address arithmetic).
+__device__ inline void dma16_s(const void* sbase, uint32_t voff, const void* lds) {
+    const uint32_t la = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+    const uint64_t b = (uint64_t)(uintptr_t)sbase;
+    // (readfirstlane returns int: widen through uint32_t, not by sign extension)
+    const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)) << 32) |
+                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(bs), "s"(la)
+                 : "memory", "m0");
+}
+
 // DMA: K/V tiles written by direct-to-LDS loads in 1 KB blocks, so rows are
 // unpadded and their 16-byte chunks XOR-swizzled by row instead.
 template <int D, bool DMA>
@@ -533,23 +548,25 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
     }
     auto dma_tile = [&](int t, int buf) {
         if constexpr (kDma) {
-            uint64_t base;   // byte offset of the wave's page (paged) or of the tile's first row (CG)
-            if constexpr (!CG) {
-                const int phys = __builtin_amdgcn_readfirstlane(max(sm.pages[4 * t + w - tbase], 0));
-                base = (uint64_t)(uint32_t)phys * page_bytes;
-            }
+            if constexpr (CG) {
 #pragma unroll
-            for (int j = 0; j < BPW; ++j) {
-                uint64_t off;
-                if constexpr (CG) {   // rows past the sequence's last are staged as the last
+                for (int j = 0; j < BPW; ++j) {   // rows past the sequence's last are staged as the last
                     const int key = min(t * BN + 16 * w + dma_row[j], L - 1);
-                    off = (uint64_t)key * row_bytes + dma_off[j];
-                } else {
-                    off = base + dma_off[j];
+                    const uint64_t off = (uint64_t)key * row_bytes + dma_off[j];
+                    const int lrow = 16 * w + j * RPB;
+                    dma16(kb + off, &sm.k[buf][lrow * KPAD]);
+                    dma16(vb + off, &sm.vt[buf][lrow * KPAD]);
                 }
-                const int lrow = 16 * w + j * RPB;
-                dma16(kb + off, &sm.k[buf][lrow * KPAD]);
-                dma16(vb + off, &sm.vt[buf][lrow * KPAD]);
+            } else {
+                // the wave's page: one scalar base per pool, 32-bit lane offsets
+                const int phys = __builtin_amdgcn_readfirstlane(max(sm.pages[4 * t + w - tbase], 0));
+                const uint64_t pbase = (uint64_t)(uint32_t)phys * page_bytes;
+#pragma unroll
+                for (int j = 0; j < BPW; ++j) {
+                    const int lrow = 16 * w + j * RPB;
+                    dma16_s(kb + pbase, dma_off[j], &sm.k[buf][lrow * KPAD]);
+                    dma16_s(vb + pbase, dma_off[j], &sm.vt[buf][lrow * KPAD]);
+                }
             }
         }
     };
