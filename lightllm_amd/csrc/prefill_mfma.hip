@@ -1187,37 +1187,57 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
     float4 acc[V4];
 #pragma unroll
     for (int v = 0; v < V4; ++v) acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int c = 0; c < nchunks; ++c) {
-        const int64_t pc = (p0 + (int64_t)c * a.Hq) * BQ + row;
-        const float l = a.part_lse[pc];
-        float4 o[V4];
-        if constexpr (HalfParts<T>::value) {
-            const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const _Float16*>(a.part_o) + pc * D) +
-                               part * (V4 / 2);
+    // CB chunks per memory round trip: every load of a batch is issued before
+    // any of its values is used (chunks past nchunks load the last one and take
+    // lse -inf), and the merge step has no branch, so the compiler cannot sink
+    // the row loads behind the lse.  A chunk whose row saw no key has lse -inf
+    // and a zero row: weight 0, no change.
+    constexpr int CB = D <= 64 ? 4 : 2;
+    constexpr int NR = HalfParts<T>::value ? V4 / 2 : V4;   // 16-byte loads per chunk row slice
+    for (int c0 = 0; c0 < nchunks; c0 += CB) {
+        float l[CB];
+        uint4 raw[CB][NR];
 #pragma unroll
-            for (int v = 0; v < V4 / 2; ++v) {
-                float f[8];
-                Chunk<_Float16>::unpack(src[v], f);
-                o[2 * v] = make_float4(f[0], f[1], f[2], f[3]);
-                o[2 * v + 1] = make_float4(f[4], f[5], f[6], f[7]);
+        for (int k = 0; k < CB; ++k) {
+            const int c = min(c0 + k, nchunks - 1);
+            const int64_t pc = (p0 + (int64_t)c * a.Hq) * BQ + row;
+            const float lk = a.part_lse[pc];
+            l[k] = c0 + k < nchunks ? lk : -INFINITY;
+            const uint4* src = HalfParts<T>::value
+                                   ? reinterpret_cast<const uint4*>(reinterpret_cast<const _Float16*>(a.part_o) + pc * D) + part * NR
+                                   : reinterpret_cast<const uint4*>(a.part_o + pc * D) + part * NR;
+#pragma unroll
+            for (int v = 0; v < NR; ++v) raw[k][v] = src[v];
+        }
+#pragma unroll
+        for (int k = 0; k < CB; ++k) {
+            float4 o[V4];
+            if constexpr (HalfParts<T>::value) {
+#pragma unroll
+                for (int v = 0; v < NR; ++v) {
+                    float f[8];
+                    Chunk<_Float16>::unpack(raw[k][v], f);
+                    o[2 * v] = make_float4(f[0], f[1], f[2], f[3]);
+                    o[2 * v + 1] = make_float4(f[4], f[5], f[6], f[7]);
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < V4; ++v) o[v] = __builtin_bit_cast(float4, raw[k][v]);
             }
-        } else {
-            const float4* src = reinterpret_cast<const float4*>(a.part_o + pc * D) + part * V4;
+            const float Mn = fmaxf(M, l[k]);
+            const bool live = Mn != -INFINITY;   // some key seen by this row so far
+            const float sc = live ? fast_exp2(M - Mn) : 1.0f;
+            const float wt = live ? fast_exp2(l[k] - Mn) : 0.0f;
+            W = fmaf(W, sc, wt);
 #pragma unroll
-            for (int v = 0; v < V4; ++v) o[v] = src[v];
+            for (int v = 0; v < V4; ++v) {
+                acc[v].x = fmaf(acc[v].x, sc, wt * o[v].x);
+                acc[v].y = fmaf(acc[v].y, sc, wt * o[v].y);
+                acc[v].z = fmaf(acc[v].z, sc, wt * o[v].z);
+                acc[v].w = fmaf(acc[v].w, sc, wt * o[v].w);
+            }
+            M = live ? Mn : M;
         }
-        const float Mn = fmaxf(M, l);
-        if (Mn == -INFINITY) continue;   // no key seen by this row yet
-        const float sc = fast_exp2(M - Mn), wt = fast_exp2(l - Mn);
-        W = fmaf(W, sc, wt);
-#pragma unroll
-        for (int v = 0; v < V4; ++v) {
-            acc[v].x = fmaf(acc[v].x, sc, wt * o[v].x);
-            acc[v].y = fmaf(acc[v].y, sc, wt * o[v].y);
-            acc[v].z = fmaf(acc[v].z, sc, wt * o[v].z);
-            acc[v].w = fmaf(acc[v].w, sc, wt * o[v].w);
-        }
-        M = Mn;
     }
     const float inv = W > 0.f ? 1.0f / W : 0.f;
     T* orow = reinterpret_cast<T*>(a.out) + ((int64_t)(q0 + q_lo + row) * a.Hq + hq) * D + part * V4 * 4;
