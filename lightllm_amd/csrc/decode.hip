@@ -200,14 +200,17 @@ struct LiveWG {
     __device__ bool operator()(int j) const { return wg_nonempty(w0 + j, T, nwg); }
 };
 
-// Merge of the balanced schedule: grid (Hq, B), one wave each.  Unit
+// Merge of the balanced schedule.  Unit
 // (b, kvh) spans positions [s, e); its segments are those of work-groups
 // wg_of(s) .. wg_of(e - 1), with ids w + u.
+// Grid (Hkv, B), one wave per q head of the kv head (G waves): the unit's
+// schedule is read once per work-group and units inside one share exit
+// together.
 template <typename T, int MD>
-__global__ __launch_bounds__(64) void decode_merge_balanced_kernel(DecodeArgs a) {
-    const int hq = blockIdx.x, b = blockIdx.y;
+__global__ __launch_bounds__(1024) void decode_merge_balanced_kernel(DecodeArgs a) {
+    const int kvh = blockIdx.x, b = blockIdx.y;
     const int G = a.Hq / a.Hkv;
-    const int kvh = hq / G, h = hq - kvh * G;
+    const int h = threadIdx.x >> 6, hq = kvh * G + h;
     const int D = a.D;
     const int Pb = a.plan[b];
     const int np = a.plan[b + 1] - Pb;
@@ -345,7 +348,8 @@ AutoChoice auto_schedule(const Kernels& ks, int B, int Hkv, int max_pages) {
 
 template <typename T, int MD>
 void launch_merge_md(bool balanced, dim3 grid, hipStream_t st, const DecodeArgs& a) {
-    if (balanced) decode_merge_balanced_kernel<T, MD><<<grid, 64, 0, st>>>(a);
+    if (balanced)
+        decode_merge_balanced_kernel<T, MD><<<dim3(a.Hkv, a.B), 64 * (a.Hq / a.Hkv), 0, st>>>(a);
     else decode_merge_kernel<T, MD><<<grid, 64, 0, st>>>(a);
 }
 
