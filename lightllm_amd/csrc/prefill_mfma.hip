@@ -167,9 +167,6 @@ __device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* orde
 #ifndef LLKV_PREFILL_INTERLEAVE
 #define LLKV_PREFILL_INTERLEAVE 1
 #endif
-#ifndef LLKV_PF_VTR
-#define LLKV_PF_VTR 1
-#endif
 #ifndef LLKV_PF_DMA
 #define LLKV_PF_DMA 1
 #endif
@@ -285,16 +282,17 @@ __device__ inline void dma16_s(const void* sbase, uint32_t voff, const void* lds
                  : "memory", "m0");
 }
 
-// DMA: K/V tiles written by direct-to-LDS loads in 1 KB blocks, so rows are
-// unpadded and their 16-byte chunks XOR-swizzled by row instead.
+// K and V tiles are row-major (key rows of D halves, KPAD apart); V's O^T
+// operand is read with transposing LDS reads.  DMA: the tiles are written by
+// direct-to-LDS loads in 1 KB blocks, so rows are unpadded and their 16-byte
+// chunks XOR-swizzled by row instead.
 template <int D, bool DMA>
 struct Smem {
-    static constexpr int KPAD = DMA ? D : D + 8;   // halves per K row (pad: spread LDS banks)
-    static constexpr int VPAD = BN + 8;   // halves per V^T row
+    static constexpr int KPAD = DMA ? D : D + 8;   // halves per K / V row (pad: spread LDS banks)
     union {
         struct {
             alignas(16) uint16_t k[2][BN * KPAD];
-            alignas(16) uint16_t vt[2][D * VPAD];
+            alignas(16) uint16_t v[2][BN * KPAD];
         };
         int order[6 * kRankUnits];   // prologue only: unit tiles, unit at each rank, q0, P, L, K/V offset
     };
@@ -310,9 +308,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
 void prefill_mfma_kernel(MfmaPrefillArgs a) {
     // Direct-to-LDS staging (head_dim 64 / 128): wave w loads page w of the
     // tile (rows 16w .. 16w + 15) of K and of V, RPB rows per 1 KB block.
-    constexpr bool kDma = LLKV_PF_DMA && LLKV_PF_VTR && (D == 64 || D == 128);
+    constexpr bool kDma = LLKV_PF_DMA && (D == 64 || D == 128);
     using SM = Smem<D, kDma>;
-    constexpr int KPAD = SM::KPAD, VPAD = SM::VPAD;
+    constexpr int KPAD = SM::KPAD;
     constexpr int CPR = D / 8;            // 16-byte chunks per row
     constexpr int RPB = 64 / CPR;         // rows per 1 KB block
     constexpr int BPW = 16 / RPB;         // blocks per wave (one page) per tile
@@ -323,8 +321,6 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
     constexpr int DT = D / 16;            // 16-dim tiles of the output
     constexpr int KCH = BN * D / 8;       // 16-byte K chunks per tile
     constexpr int KCH_T = KCH / 256;      // per thread
-    constexpr int VT_N = (BN / 2) * (D / 8);          // V tasks (2 keys x 8 dims) per tile
-    constexpr int VT_T = (VT_N + 255) / 256;          // per thread (head_dim 96: the last partly idle)
     __shared__ SM sm;
 
     const int tid = threadIdx.x;
@@ -388,17 +384,9 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
 
     // ---- staging: global -> registers -> LDS -----------------------------
     int tbase = 0;   // first page id held in sm.pages
-    u32x4 kr[KCH_T];
-#if LLKV_PF_VTR
-    // V is staged like K (row-major, K's row stride) and read transposed by
-    // ds_read_b64_tr_b16; its rows share K's page addresses.
-    using VReg = u32x4[KCH_T];
-#else
-    using VReg = u32x4[VT_T][2];
-#endif
-    VReg vr;
-    static_assert(!LLKV_PF_VTR || D * VPAD >= BN * KPAD, "row-major V tile fits the V^T buffer");
-    static_assert(KCH % 256 == 0, "K chunks spread evenly over the threads");
+    // V is staged like K (row-major, the same row offsets and page addresses).
+    u32x4 kr[KCH_T], vr[KCH_T];
+    static_assert(KCH % 256 == 0, "K / V chunks spread evenly over the threads");
     // Per-thread byte offsets inside a page and page slot of each staged row;
     // a load is then base + phys * page_bytes + offset (one 32x32->64 multiply-add).
     // Contiguous K/V: the key within the tile and the byte offset in the row.
@@ -415,37 +403,15 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
         kslot[j] = CG ? key : key >> 4;
         koff[j] = (CG ? 0u : (uint32_t)(key & 15) * row_bytes) + (uint32_t)c * 16u;
     }
-#if !LLKV_PF_VTR
-    uint32_t voff[VT_T];
-    int vslot[VT_T];
-#pragma unroll
-    for (int j = 0; j < VT_T; ++j) {
-        const int task = (VT_N % 256 == 0 || tid + 256 * j < VT_N) ? tid + 256 * j : 0;   // idle: task 0's rows
-        const int kp = task % (BN / 2), c = task / (BN / 2);
-        vslot[j] = CG ? 2 * kp : (2 * kp) >> 4;
-        voff[j] = (CG ? 0u : (uint32_t)((2 * kp) & 15) * row_bytes) + (uint32_t)c * 16u;
-    }
-#endif
-    auto load_tile = [&](int t, u32x4 (&kreg)[KCH_T], VReg& vreg) {
+    auto load_tile = [&](int t, u32x4 (&kreg)[KCH_T], u32x4 (&vreg)[KCH_T]) {
         if constexpr (CG) {   // rows past the sequence's last are staged as the last
             const int key0 = t * BN, last = L - 1;
 #pragma unroll
             for (int j = 0; j < KCH_T; ++j) {
                 const uint64_t off = (uint64_t)min(key0 + kslot[j], last) * row_bytes + koff[j];
                 kreg[j] = *reinterpret_cast<const u32x4*>(kb + off);
-#if LLKV_PF_VTR
                 vreg[j] = *reinterpret_cast<const u32x4*>(vb + off);
-#endif
             }
-#if !LLKV_PF_VTR
-#pragma unroll
-            for (int j = 0; j < VT_T; ++j) {
-                vreg[j][0] = *reinterpret_cast<const u32x4*>(
-                    vb + (uint64_t)min(key0 + vslot[j], last) * row_bytes + voff[j]);
-                vreg[j][1] = *reinterpret_cast<const u32x4*>(
-                    vb + (uint64_t)min(key0 + vslot[j] + 1, last) * row_bytes + voff[j]);
-            }
-#endif
             return;
         }
         // pages past the sequence's last are staged as the last page (valid memory)
@@ -454,48 +420,17 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
         for (int j = 0; j < KCH_T; ++j) {
             const uint64_t off = (uint64_t)(uint32_t)max(pg[kslot[j]], 0) * page_bytes + koff[j];
             kreg[j] = *reinterpret_cast<const u32x4*>(kb + off);
-#if LLKV_PF_VTR
             vreg[j] = *reinterpret_cast<const u32x4*>(vb + off);
-#endif
         }
-#if !LLKV_PF_VTR
-#pragma unroll
-        for (int j = 0; j < VT_T; ++j) {
-            const uint64_t phys = (uint32_t)max(pg[vslot[j]], 0);
-            const char* p = vb + phys * page_bytes + voff[j];
-            vreg[j][0] = *reinterpret_cast<const u32x4*>(p);
-            vreg[j][1] = *reinterpret_cast<const u32x4*>(p + row_bytes);
-        }
-#endif
     };
-    auto store_tile = [&](int buf, const u32x4 (&kreg)[KCH_T], const VReg& vreg) {
+    auto store_tile = [&](int buf, const u32x4 (&kreg)[KCH_T], const u32x4 (&vreg)[KCH_T]) {
 #pragma unroll
         for (int j = 0; j < KCH_T; ++j) {
             const int ch = tid + 256 * j;
             const int key = ch / (D / 8), c = ch % (D / 8);
             *reinterpret_cast<u32x4*>(&sm.k[buf][key * KPAD + c * 8]) = kreg[j];
-#if LLKV_PF_VTR
-            *reinterpret_cast<u32x4*>(&sm.vt[buf][key * KPAD + c * 8]) = vreg[j];
-#endif
+            *reinterpret_cast<u32x4*>(&sm.v[buf][key * KPAD + c * 8]) = vreg[j];
         }
-#if !LLKV_PF_VTR
-#pragma unroll
-        for (int j = 0; j < VT_T; ++j) {
-            const int task = tid + 256 * j;
-            if (VT_N % 256 != 0 && task >= VT_N) break;
-            const int kp = task % (BN / 2), c = task / (BN / 2);
-            // keys 2kp (v0) and 2kp+1 (v1), dims 8c..8c+7: dim e's pair (v0[e], v1[e]) is one
-            // dword of V^T, built with v_perm_b32 (low halves: 0x05040100, high: 0x07060302)
-            const uint32_t a0[4] = {vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w};
-            const uint32_t a1[4] = {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w};
-            uint32_t* dst = reinterpret_cast<uint32_t*>(&sm.vt[buf][(c * 8) * VPAD + 2 * kp]);
-#pragma unroll
-            for (int e2 = 0; e2 < 4; ++e2) {
-                dst[(2 * e2) * (VPAD / 2)] = __builtin_amdgcn_perm(a1[e2], a0[e2], 0x05040100u);
-                dst[(2 * e2 + 1) * (VPAD / 2)] = __builtin_amdgcn_perm(a1[e2], a0[e2], 0x07060302u);
-            }
-        }
-#endif
     };
     // Half-column hc of tile row `row` in LDS: with DMA the 16-byte chunk
     // index is XOR-ed with the row (mod the chunks per row).
@@ -505,7 +440,6 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
     };
     // A operand of O^T = V^T P^T for output dims dt*16 .. +15 and the 32-key
     // half ss: lane (g, c16) holds dim dt*16 + c16 of keys 32 ss + 8 g .. + 7.
-#if LLKV_PF_VTR
     // ds_read_b64_tr_b16 within each 16-lane group: output lane 4a + e gets
     // element e of the 4 halves addressed by lanes a, a + 4, a + 8, a + 12; so
     // lane c16 addresses row (key) c16 / 4, dims 4 (c16 % 4) .. + 3, and each
@@ -514,18 +448,13 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
         typedef short s16x4 __attribute__((ext_vector_type(4)));
         const int r0 = 32 * ss + 8 * g + (c16 >> 2), hc = dt * 16 + 4 * (c16 & 3);
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(&sm.vt[buf][r0 * KPAD + scol(r0, hc)]));
+            (__attribute__((address_space(3))) s16x4*)(&sm.v[buf][r0 * KPAD + scol(r0, hc)]));
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(&sm.vt[buf][(r0 + 4) * KPAD + scol(r0 + 4, hc)]));
+            (__attribute__((address_space(3))) s16x4*)(&sm.v[buf][(r0 + 4) * KPAD + scol(r0 + 4, hc)]));
         typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
         const u32x2v l2 = __builtin_bit_cast(u32x2v, lo), h2 = __builtin_bit_cast(u32x2v, hi);
         return make_uint4(l2.x, l2.y, h2.x, h2.y);
     };
-#else
-    auto v_operand = [&](int buf, int dt, int ss) {
-        return *reinterpret_cast<const uint4*>(&sm.vt[buf][(dt * 16 + c16) * VPAD + 32 * ss + 8 * g]);
-    };
-#endif
 
     // Page ids live in LDS so that no K/V load waits behind a table load.
     auto stage_pages = [&](int base) {
@@ -555,7 +484,7 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
                     const uint64_t off = (uint64_t)key * row_bytes + dma_off[j];
                     const int lrow = 16 * w + j * RPB;
                     dma16(kb + off, &sm.k[buf][lrow * KPAD]);
-                    dma16(vb + off, &sm.vt[buf][lrow * KPAD]);
+                    dma16(vb + off, &sm.v[buf][lrow * KPAD]);
                 }
             } else {
                 // the wave's page: one scalar base per pool, 32-bit lane offsets
@@ -565,7 +494,7 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 for (int j = 0; j < BPW; ++j) {
                     const int lrow = 16 * w + j * RPB;
                     dma16_s(kb + pbase, dma_off[j], &sm.k[buf][lrow * KPAD]);
-                    dma16_s(vb + pbase, dma_off[j], &sm.vt[buf][lrow * KPAD]);
+                    dma16_s(vb + pbase, dma_off[j], &sm.v[buf][lrow * KPAD]);
                 }
             }
         }
