@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "prefill_mfma.h"
 
@@ -164,6 +165,9 @@ __device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* orde
         }                                                  \
     } while (0)
 
+#ifndef LLKV_PF_UNROLL2
+#define LLKV_PF_UNROLL2 1
+#endif
 #ifndef LLKV_PREFILL_INTERLEAVE
 #define LLKV_PREFILL_INTERLEAVE 1
 #endif
@@ -512,8 +516,11 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
     }
     __syncthreads();
 
-    for (int t = t_begin; t < t_end; ++t) {
-        const int buf = (t - t_begin) & 1;
+    // One key tile; buf = (t - t_begin) & 1.  The loop below runs it twice per
+    // trip with buf as a compile-time constant, so the LDS addresses of both
+    // buffers fold into the instructions' offsets.
+    auto tile_step = [&](int t, auto bufc) {
+        const int buf = static_cast<int>(bufc);
         if (t + 1 < t_end) {
             // tile t+1 covers pages [4(t+1), 4(t+1)+4); restage when they leave the window
             // (uniform branch; every earlier read of sm.pages preceded the last barrier)
@@ -681,7 +688,19 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
             if (t + 1 < t_end) store_tile(buf ^ 1, kr, vr);
         }
         __syncthreads();
+    };
+#if LLKV_PF_UNROLL2
+    {
+        int t = t_begin;
+        for (; t + 1 < t_end; t += 2) {
+            tile_step(t, std::integral_constant<int, 0>());
+            tile_step(t + 1, std::integral_constant<int, 1>());
+        }
+        if (t < t_end) tile_step(t, std::integral_constant<int, 0>());
     }
+#else
+    for (int t = t_begin; t < t_end; ++t) tile_step(t, (t - t_begin) & 1);
+#endif
 
     // ---- normalise and write: lane holds dims dt*16 + 4g + i of its query --
     // (one chunk: the output row; several: an fp32 partial row + log2-sum-exp2,
