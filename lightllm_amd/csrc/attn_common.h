@@ -73,6 +73,7 @@ __device__ inline void lds_barrier() {
 }
 
 constexpr int kDecodeWaves = 4;   // waves per decode work-group
+constexpr int kUnitWaves = 16;    // waves per work-group of the unit schedule (one work-group per unit)
 
 constexpr float kNegBig = -1e30f;   // finite "minus infinity" for running maxima
 

@@ -9,10 +9,14 @@ namespace llkv {
 
 typedef void (*DecodeFn)(DecodeArgs);
 
-// The two schedules of one MFMA body: fixed split and balanced.
+// The schedules of one MFMA body: fixed split and balanced (kDecodeWaves
+// waves per work-group), and unit: the fixed-split kernel with kUnitWaves
+// waves per work-group, launched with one split (no partials, no merge) for
+// small batches of short sequences.
 struct Kernels {
     DecodeFn split = nullptr;
     DecodeFn balanced = nullptr;
+    DecodeFn unit = nullptr;
 };
 
 // Tuned kernels for head_dim D and G query heads per kv head, plain or with

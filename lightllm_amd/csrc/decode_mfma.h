@@ -136,13 +136,16 @@ template <int D> struct ScoreOps<bf16_t, D> : ScoreOps16<bf16_t, D> {};
 // A = true: the fused-append variant (llkv_paged_decode_append), which reads
 // the segment's new token from the caller's buffers; the plain variant's page
 // loop has no trace of it.
-template <typename TT, int D, int G, bool A = false>
+// WV: waves per work-group (kDecodeWaves; kUnitWaves for the one-work-group-
+// per-unit schedule of small batches).
+template <typename TT, int D, int G, bool A = false, int WV = kDecodeWaves>
 struct MfmaDecode {
     static_assert(G >= 1 && G <= 16, "up to 16 query heads per KV head");
     static_assert(D % 32 == 0, "head_dim multiple of 32");
     using T = TT;
     using Ops = ScoreOps<T, D>;
-    static constexpr int W = kDecodeWaves;    // waves per work-group
+    static constexpr int W = WV;              // waves per work-group
+    static constexpr int kThreads = 64 * W;
     // V is loaded in 64-dim groups (h), lane c holding dims 64h + 4c .. + 3;
     // with head_dim 96 the last group is half empty (lanes c >= 8 load none).
     static constexpr int VH = (D + 63) / 64;  // V vectors per lane per token
@@ -158,9 +161,12 @@ struct MfmaDecode {
     // Resident waves per SIMD the register budget is held to: 5 (<= 96
     // registers) for head_dim 64; head_dim 128 needs more and gets 4.
     // head_dim 256: ~200 VGPRs (two waves per SIMD, no spills; three spill 33-49).
-    static constexpr int kWavesPerEU = D == 64 ? 5 : (D == 96 ? 3 : (D == 128 ? 4 : 2));
+    // The unit schedule's 16-wave work-group puts four waves on each SIMD.
+    static constexpr int kWavesPerEU =
+        W > kDecodeWaves ? 4 : (D == 64 ? 5 : (D == 96 ? 3 : (D == 128 ? 4 : 2)));
     // Segments per round: two where the LDS for the parked states stays small.
-    static constexpr int kSegMax = G * D <= 512 ? 2 : 1;
+    // (The unit schedule runs one segment per work-group.)
+    static constexpr int kSegMax = (W == kDecodeWaves && G * D <= 512) ? 2 : 1;
 
     struct Smem {
         float acc[kSegMax][W][G][D];

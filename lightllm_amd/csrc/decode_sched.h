@@ -15,10 +15,10 @@
 namespace llkv {
 namespace {
 
-// Fixed split schedule: grid (S_max, Hkv, B), 4 waves per work-group, one
-// segment each.
+// Fixed split schedule: grid (S_max, Hkv, B), Body::W waves per work-group,
+// one segment each.
 template <class Body>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Body::kWavesPerEU)))
+__global__ __launch_bounds__(Body::kThreads) __attribute__((amdgpu_waves_per_eu(Body::kWavesPerEU)))
 void decode_split_kernel(DecodeArgs a) {
     __shared__ typename Body::Smem sm;
     __shared__ SegDesc segs[1];
@@ -110,19 +110,30 @@ Kernels kernels_of() {
     return k;
 }
 
+// head_dim 64 / 128 also get the unit schedule's kUnitWaves-wave kernel,
+// except fp32 at head_dim 128, whose body does not fit the 128 registers of
+// four waves per SIMD (~50 would spill).
+template <typename T, int D, int G, bool A>
+Kernels kernels_with_unit() {
+    Kernels k = kernels_of<MfmaDecode<T, D, G, A>>();
+    if constexpr (!(Elem<T>::kDtype == LLKV_DTYPE_F32 && D == 128))
+        k.unit = decode_split_kernel<MfmaDecode<T, D, G, A, kUnitWaves>>;
+    return k;
+}
+
 template <typename T, int D, bool A>
 Kernels tuned_g(int G) {
     switch (G) {
-        case 1: return kernels_of<MfmaDecode<T, D, 1, A>>();
-        case 2: return kernels_of<MfmaDecode<T, D, 2, A>>();
-        case 3: return kernels_of<MfmaDecode<T, D, 3, A>>();
-        case 4: return kernels_of<MfmaDecode<T, D, 4, A>>();
-        case 5: return kernels_of<MfmaDecode<T, D, 5, A>>();
-        case 6: return kernels_of<MfmaDecode<T, D, 6, A>>();
-        case 7: return kernels_of<MfmaDecode<T, D, 7, A>>();
-        case 8: return kernels_of<MfmaDecode<T, D, 8, A>>();
-        case 12: return kernels_of<MfmaDecode<T, D, 12, A>>();
-        case 16: return kernels_of<MfmaDecode<T, D, 16, A>>();
+        case 1: return kernels_with_unit<T, D, 1, A>();
+        case 2: return kernels_with_unit<T, D, 2, A>();
+        case 3: return kernels_with_unit<T, D, 3, A>();
+        case 4: return kernels_with_unit<T, D, 4, A>();
+        case 5: return kernels_with_unit<T, D, 5, A>();
+        case 6: return kernels_with_unit<T, D, 6, A>();
+        case 7: return kernels_with_unit<T, D, 7, A>();
+        case 8: return kernels_with_unit<T, D, 8, A>();
+        case 12: return kernels_with_unit<T, D, 12, A>();
+        case 16: return kernels_with_unit<T, D, 16, A>();
     }
     return Kernels();
 }

@@ -243,6 +243,10 @@ FUSED = [
     ("f32_G5_S3", 20, 10, 2, 64, torch.float32, 3, (1, 900)),
     ("f16_D256_G2_auto", 24, 16, 8, 256, torch.float16, 0, (1, 2500)),
     ("f32_D96_MHA_auto", 30, 8, 8, 96, torch.float32, 0, (1, 1200)),
+    # the unit schedule (one 16-wave work-group per sequence and kv head, no merge)
+    ("f32_G7_unit_auto", 64, 14, 2, 64, torch.float32, 0, (1, 250)),
+    ("f16_llama_unit_auto", 32, 32, 8, 128, torch.float16, 0, (1, 256)),
+    ("bf16_G7_S1_unit_long", 4, 14, 2, 64, torch.bfloat16, 1, (500, 3000)),
 ]
 
 
@@ -462,6 +466,43 @@ def test_decode_edge_cases(name, hq, hkv, d, lengths, dtype):
         else:
             check_lowp(out, ref, f"{name} S={s}", 2e-3 if dtype == torch.float16 else 1.6e-2)
         case.k_pool, case.v_pool = kp.cpu(), vp.cpu()
+
+
+UNIT = [
+    # (name, hq, hkv, d, B, max length, num_splits, dtype): automatic choices that take the
+    # unit schedule (at least 64 units for one page per wave, 128 for two), and S = 1
+    ("f32_G7_one_page", 14, 2, 64, 64, 256, 0, torch.float32),
+    ("f32_G7_two_pages", 14, 2, 64, 64, 512, 0, torch.float32),
+    ("f16_D128_G4", 32, 8, 128, 32, 256, 0, torch.float16),
+    ("bf16_G7_B128", 14, 2, 64, 128, 256, 0, torch.bfloat16),
+    ("f16_D128_G16_B128", 16, 1, 128, 128, 512, 0, torch.float16),
+    ("f32_G7_S1_long", 14, 2, 64, 3, 5000, 1, torch.float32),
+    ("f16_D64_S1_long", 8, 2, 64, 5, 3000, 1, torch.float16),
+    ("f32_D128_S1_split_kernel", 8, 2, 128, 6, 700, 1, torch.float32),
+]
+
+
+@pytest.mark.parametrize("name,hq,hkv,d,B,lmax,S,dtype", UNIT, ids=[u[0] for u in UNIT])
+def test_decode_unit_schedule(name, hq, hkv, d, B, lmax, S, dtype):
+    """Small batches of short sequences (and explicit S = 1): one 16-wave work-group per
+    (sequence, kv head) writes the output directly.  Lengths include 0, 1, 16 and 17."""
+    g = torch.Generator().manual_seed(len(name) * 7)
+    lengths = torch.randint(1, lmax + 1, (B,), generator=g).tolist()
+    lengths[0] = lmax
+    for i, L in enumerate([0, 1, 16, 17]):
+        if i + 1 < B:
+            lengths[i + 1] = L
+    say(f"decode unit schedule {name}: B={B} Hq={hq} Hkv={hkv} D={d} max L={max(lengths)} S={S} {dtype}")
+    need = sum((L + 15) // 16 for L in lengths) + 4
+    case = wl.decode_case(name, B, hq, hkv, d, lengths, need, dtype, seed=len(name), append=False)
+    out, _, _ = run_decode(case, num_splits=S, append=False)
+    ref = oracle_decode(case, np_pool(case.k_pool), np_pool(case.v_pool))
+    if dtype == torch.float32:
+        check_fp32(out, ref, name)
+    else:
+        check_lowp(out, ref, name, 2e-3 if dtype == torch.float16 else 1.6e-2)
+    if B > 1:
+        assert torch.count_nonzero(out[1]).item() == 0, "empty sequence"
 
 
 BALANCE = [
