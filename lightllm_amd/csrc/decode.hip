@@ -323,35 +323,51 @@ constexpr int kShortChainPages = 4;   // pages per wave up to which a split is l
 
 struct AutoChoice {
     bool balanced;
+    bool wide;    // one split on the kUnitWaves-wave kernel (unit schedule)
     int splits;   // fixed schedule: S
 };
 
-// Unit schedule: one kUnitWaves-wave work-group per (sequence, kv head),
-// launched as the fixed split with S = 1, so the output is written directly
-// and no merge kernel runs.  Used when every wave has at most
-// kUnitPagesPerWave pages, there are at least kUnitMinUnits units per page
-// of a wave's chain (with fewer, splits that give every wave a single page are
-// faster despite the merge: B = 1, 512 tokens, 7.5 against 10.3 us; 32 x 512
-// tokens 9.2 against 10.8 us) and they fit in one resident set.  Measured
-// (unit against the previous choice): 32 x 256 tokens, Llama-3 heads, fp16
-// 15.6 -> 9.7 us; 128 x 256 tokens, 14/2/64 bf16 11.1 -> 7.3 us; 64 x 128
-// fp32 7.9 -> 6.2 us; 64 x 512 fp32 12.2 -> 11.5 us.
-constexpr int kUnitPagesPerWave = 2;
-constexpr int kUnitMinUnits = 64;
+// Choice of the automatic schedule, from a sweep of batch size (16 .. 1024),
+// context (64 .. 1024 tokens, lengths uniform in [L/2, L]) and two head layouts
+// (14/2/64 fp32, 32/8/128 fp16), every shape timed under each schedule:
+//  * one split per (sequence, kv head) on 4-wave work-groups, no merge, when
+//    every sequence is short (<= kOneSplitShortPages pages), or when there are
+//    many units and no sequence is long (the balanced schedule's scan, segment
+//    bookkeeping and merge cost more than the page chain it shortens):
+//    e.g. 512 x 128 tokens fp32 31.5 -> 13.7 us, 1024 x 64 Llama-3 fp16
+//    87 -> 52 us, 256 x 1024 fp32 45 -> 37 us;
+//  * the unit schedule (one split on 16-wave work-groups) for a middle range of
+//    units with up to 4 pages per wave: 32 x 1024 Llama-3 fp16 30.6 -> 23.4 us,
+//    128 x 1024 fp32 24.7 -> 20.9 us;
+//  * otherwise the balanced schedule for many units (long or uneven contexts:
+//    configuration 5) and fixed splits for few (configurations 1-3).
+constexpr int kOneSplitShortPages = 8;
+constexpr int kOneSplitMaxPages = 64;
+constexpr int kOneSplitMinUnits = 384;        // up to kOneSplitMaxPages pages
+constexpr int kOneSplitMinUnitsShort = 256;   // up to 16 pages
+constexpr int kUnitMaxChain = 4;              // pages per wave of the unit schedule
+constexpr int kUnitMinUnits = 64;             // units per page of a wave's chain
 
 bool unit_schedule(const Kernels& ks, int B, int Hkv, int max_pages) {
     const int64_t units = (int64_t)B * Hkv;
     const int chain = (std::max(1, max_pages) + kUnitWaves - 1) / kUnitWaves;   // pages per wave
-    if (ks.unit == nullptr || chain > kUnitPagesPerWave || units < (int64_t)kUnitMinUnits * chain)
+    if (ks.unit == nullptr || chain > kUnitMaxChain || units < (int64_t)kUnitMinUnits * chain)
         return false;
     const int cap = resident_workgroups(reinterpret_cast<const void*>(ks.unit), 64 * kUnitWaves);
     return units <= cap;
 }
 
 AutoChoice auto_schedule(const Kernels& ks, int B, int Hkv, int max_pages) {
-    AutoChoice c{false, 0};
+    AutoChoice c{false, false, 0};
     const int64_t units = (int64_t)B * Hkv;
+    if (max_pages <= kOneSplitShortPages ||
+        (max_pages <= kOneSplitMaxPages && units >= kOneSplitMinUnits) ||
+        (max_pages <= 16 && units >= kOneSplitMinUnitsShort)) {
+        c.splits = 1;
+        return c;
+    }
     if (unit_schedule(ks, B, Hkv, max_pages)) {
+        c.wide = true;
         c.splits = 1;
         return c;
     }
@@ -470,11 +486,14 @@ int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_ne
         ks = pick_tuned(dtype, head_dim, G, k_new != nullptr);
     }
     const int max_pages_hint = (max_seq_len + block_size - 1) / block_size;
-    bool balanced = false;
+    bool balanced = false, wide = false;
     if (num_splits == 0 && ks.split != nullptr) {
         const AutoChoice c = auto_schedule(ks, num_seqs, num_kv_heads, max_pages_hint);
         balanced = c.balanced;
+        wide = c.wide;
         if (!balanced) num_splits = c.splits;
+    } else if (num_splits == 1 && ks.split != nullptr) {
+        wide = unit_schedule(ks, num_seqs, num_kv_heads, max_pages_hint);
     }
 
     DecodeArgs a;
@@ -526,7 +545,7 @@ int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_ne
         a.fixed_S = p.fixed_S;
         if (ks.split) {
             dim3 grid(p.S_max, num_kv_heads, num_seqs);
-            if (p.S_max == 1 && ks.unit != nullptr)   // one split: the unit schedule's wider work-groups
+            if (wide && p.S_max == 1)   // the unit schedule's wider work-groups
                 ks.unit<<<grid, 64 * kUnitWaves, 0, st>>>(a);
             else
                 ks.split<<<grid, 64 * kDecodeWaves, 0, st>>>(a);

@@ -479,13 +479,19 @@ UNIT = [
     ("f32_G7_S1_long", 14, 2, 64, 3, 5000, 1, torch.float32),
     ("f16_D64_S1_long", 8, 2, 64, 5, 3000, 1, torch.float16),
     ("f32_D128_S1_split_kernel", 8, 2, 128, 6, 700, 1, torch.float32),
+    # automatic choices of one split on 4-wave work-groups (many units, no long sequence;
+    # more units than one resident set) and of the 16-wave unit kernel (4 pages per wave)
+    ("f16_llama_B300_one_split", 32, 8, 128, 300, 400, 0, torch.float16),
+    ("f32_G7_B256_L1024_one_split", 14, 2, 64, 256, 1024, 0, torch.float32),
+    ("f16_llama_B32_L1024_unit", 32, 8, 128, 32, 1024, 0, torch.float16),
 ]
 
 
 @pytest.mark.parametrize("name,hq,hkv,d,B,lmax,S,dtype", UNIT, ids=[u[0] for u in UNIT])
 def test_decode_unit_schedule(name, hq, hkv, d, B, lmax, S, dtype):
-    """Small batches of short sequences (and explicit S = 1): one 16-wave work-group per
-    (sequence, kv head) writes the output directly.  Lengths include 0, 1, 16 and 17."""
+    """Automatic choices of one split per (sequence, kv head), on 4-wave or 16-wave
+    work-groups, and explicit S = 1: the output is written directly, with no merge.
+    Lengths include 0, 1, 16 and 17."""
     g = torch.Generator().manual_seed(len(name) * 7)
     lengths = torch.randint(1, lmax + 1, (B,), generator=g).tolist()
     lengths[0] = lmax
