@@ -180,6 +180,8 @@ int check_launch(const char* what);
 // Work-groups of `threads` threads of kernel `fn` the current device holds at
 // once (compute units x resident work-groups per unit), cached per device.
 int resident_workgroups(const void* fn, int threads);
+// Compute units of the current device (cached per device).
+int device_cus();
 inline size_t dtype_bytes(int dtype) {
     return dtype == LLKV_DTYPE_F32 ? 4 : (dtype == LLKV_DTYPE_F16 || dtype == LLKV_DTYPE_BF16) ? 2 : 0;
 }

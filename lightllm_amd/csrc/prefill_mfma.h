@@ -25,8 +25,10 @@
 // work-groups, the q heads of one kv head on one XCD), so that a cached prefix of thousands of keys does not
 // serialise on one work-group; their partials (normalised rows, fp16 for
 // fp16 pools and fp32 otherwise, + fp32 log2-sum-exp2) are merged by
-// prefill_merge_kernel.  The split is chosen on
-// the host from the shape bounds and the kernel's resident work-group count.
+// prefill_merge_kernel.  The host plans the split from the shape bounds and the
+// kernel's resident work-group count; the kernel then drops it when the units'
+// actual key lengths are even enough (no unit longer than the average load of
+// a compute unit), and the merge kernel follows that decision.
 #pragma once
 
 #include "attn_common.h"
@@ -59,6 +61,10 @@ struct MfmaPrefillArgs {
     int groups;       // N * qblocks * max_chunks * Hkv (chunk slot, kv head) work items
     float* part_o;    // [N*qblocks*max_chunks*Hq][BQ][D] (max_chunks > 1), fp16 elements for fp16 pools
     float* part_lse;  // [N*qblocks*max_chunks*Hq][BQ]
+    // Split decision made on the device from the units' key lengths (max_chunks > 1):
+    // plan_flag (workspace header) receives 1 when the launch runs unsplit after all.
+    int* plan_flag;
+    int n_cus;        // compute units of the device
 };
 
 // Workspace bytes for the chunked schedule (0: the shape runs unchunked).

@@ -105,18 +105,19 @@ __device__ inline UnitInfo unit_info(const MfmaPrefillArgs& a, int u) {
 
 // Units ranked by key tiles (descending, ties by index) for up to kRankUnits
 // units; larger batches keep index order.  Every thread of the work-group
-// calls it (it contains barriers).  Returns the unit of the given rank and
-// its UnitInfo (read back from LDS, so that the unit's lengths cost no second
-// global round trip).
+// calls rank_units (it contains barriers); it leaves in LDS each unit's tiles
+// and lengths (so the chosen unit costs no second global round trip) and the
+// unit at each rank, and returns the split decision: true when the host's key
+// split is dropped because no unit has more key tiles than a compute unit's
+// share of the whole launch (sum of tiles x Hq / CUs).  Such even loads run
+// best unsplit (one work-group per unit, no partials or merge); uneven ones,
+// where the longest unit would set the time, keep the split.
 constexpr int kRankUnits = 1024;
 
-__device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* order,
-                                   UnitInfo& info) {
+__device__ inline bool rank_units(const MfmaPrefillArgs& a, int* order) {
+    __shared__ int s_plan[2];   // sum of the units' tiles, longest unit's tiles
     const int U = a.N * a.qblocks;
-    if (U > kRankUnits) {
-        info = unit_info(a, rank);
-        return rank;
-    }
+    if (U > kRankUnits) return false;
     int* tiles = order;
     int* at = order + kRankUnits;
     int* q0s = order + 2 * kRankUnits;
@@ -132,19 +133,37 @@ __device__ inline int unit_by_rank(const MfmaPrefillArgs& a, int rank, int* orde
         kvos[u] = r.kvo;
     }
     __syncthreads();
+    // The rank pass reads every unit's tiles: unit 0's thread also sums them, and
+    // the thread of rank 0 holds the longest.
     for (int u = threadIdx.x; u < U; u += blockDim.x) {
         const int tu = tiles[u];
-        int r = 0;
-        for (int v = 0; v < U; ++v) r += (tiles[v] > tu) | ((tiles[v] == tu) & (v < u));
+        int r = 0, sum = 0;
+        for (int v = 0; v < U; ++v) {
+            const int tv = tiles[v];
+            r += (tv > tu) | ((tv == tu) & (v < u));
+            sum += tv;
+        }
         at[r] = u;
+        if (u == 0) s_plan[0] = sum;
+        if (r == 0) s_plan[1] = tu;
     }
     __syncthreads();
-    const int u = at[rank];
-    info.q0 = q0s[u];
-    info.P = ps[u];
-    info.L = ls[u];
-    info.kvo = kvos[u];
-    info.tiles = tiles[u];
+    return a.max_chunks > 1 && (int64_t)s_plan[1] * a.n_cus <= (int64_t)s_plan[0] * a.Hq;
+}
+
+// The unit at `rank` (after rank_units) and its UnitInfo.
+__device__ inline int ranked_unit(const MfmaPrefillArgs& a, int rank, const int* order,
+                                  UnitInfo& info) {
+    if (a.N * a.qblocks > kRankUnits) {
+        info = unit_info(a, rank);
+        return rank;
+    }
+    const int u = order[kRankUnits + rank];
+    info.q0 = order[2 * kRankUnits + u];
+    info.P = order[3 * kRankUnits + u];
+    info.L = order[4 * kRankUnits + u];
+    info.kvo = order[5 * kRankUnits + u];
+    info.tiles = order[u];
     return u;
 }
 
@@ -214,10 +233,22 @@ __device__ inline bool take_work(const MfmaPrefillArgs& a, int* order, Work& wk)
     const int y = blockIdx.x / a.Hq;
     if (y * a.Hkv >= a.groups) return false;
 #endif
-    const int slot = y / a.max_chunks;
-    wk.ci = y - slot * a.max_chunks;   // key chunk of the unit
+    // Every work-group takes the same decision from the same lengths.  Unsplit,
+    // the first N x qblocks chunk slots are the units themselves (chunk 0) and
+    // the other work-groups have nothing to do.
+    const bool unsplit = rank_units(a, order);
+    if (blockIdx.x == 0 && threadIdx.x == 0 && a.plan_flag != nullptr) *a.plan_flag = unsplit ? 1 : 0;
+    int slot;
+    if (unsplit) {
+        if (y >= a.N * a.qblocks) return false;
+        slot = y;
+        wk.ci = 0;
+    } else {
+        slot = y / a.max_chunks;
+        wk.ci = y - slot * a.max_chunks;   // key chunk of the unit
+    }
     UnitInfo ui;
-    wk.unit = unit_by_rank(a, slot, order, ui);  // (sequence, query block)
+    wk.unit = ranked_unit(a, slot, order, ui);  // (sequence, query block)
     wk.n = wk.unit / a.qblocks;
     const int qb = a.qblocks - 1 - (wk.unit % a.qblocks);
     wk.q0 = ui.q0;
@@ -232,7 +263,7 @@ __device__ inline bool take_work(const MfmaPrefillArgs& a, int* order, Work& wk)
     const int ntiles = (wk.kend + BN - 1) / BN;
     // at most max_chunks chunks (a max_seq_len bound below a length): the last
     // one takes the remaining tiles
-    const int nchunks = min((ntiles + a.chunk_tiles - 1) / a.chunk_tiles, a.max_chunks);
+    const int nchunks = unsplit ? 1 : min((ntiles + a.chunk_tiles - 1) / a.chunk_tiles, a.max_chunks);
     if (wk.ci > 0 && wk.ci >= nchunks) return false;   // chunk 0 also covers an empty key range (zeros)
     wk.t_begin = wk.ci * a.chunk_tiles;
     wk.t_end = wk.ci == nchunks - 1 ? ntiles : min(wk.t_begin + a.chunk_tiles, ntiles);
@@ -1115,6 +1146,9 @@ __device__ inline void store4<float>(float* p, float x, float y, float z, float 
 // log-sum-exp (each chunk's lse and row slice are loaded together).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
+    // The main kernel's split decision; loaded together with the lengths below
+    // and checked before anything is read or written.
+    const int unsplit = *a.plan_flag;
     constexpr int TPR = 256 / BQ;     // threads per row
     constexpr int V4 = D / TPR / 4;   // float4 per thread
     const int hq = blockIdx.x, unit = blockIdx.y;
@@ -1122,6 +1156,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
     const int qb = a.qblocks - 1 - (unit % a.qblocks);
     int q0, P, L, kvo, hist;
     seq_geom(a, n, q0, P, L, kvo, hist);
+    if (unsplit != 0) return;   // every row was written by the main kernel
     const int q_lo = qb * BQ;
     const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
     if (q_lo + row >= P) return;
@@ -1264,6 +1299,10 @@ PrefillFn merge_kernel(int dtype, int head_dim) {
     return merge_for<bf16_t>(head_dim);
 }
 
+// Workspace header: the main kernel's split decision (one int), read by the
+// merge kernel.
+constexpr size_t kPlanHeaderBytes = 256;
+
 struct ChunkPlan {
     int qblocks, max_chunks, chunk_tiles;
 };
@@ -1297,7 +1336,7 @@ size_t prefill_mfma_workspace(int N, int Hq, int head_dim, int block_size, int d
     if (c.max_chunks <= 1) return 0;
     const size_t parts = (size_t)N * c.qblocks * c.max_chunks * Hq;
     const size_t part_elem = (dtype == LLKV_DTYPE_F16 && HalfParts<_Float16>::value) ? 2 : sizeof(float);
-    return parts * BQ * sizeof(float) + parts * BQ * head_dim * part_elem;
+    return kPlanHeaderBytes + parts * BQ * sizeof(float) + parts * BQ * head_dim * part_elem;
 }
 
 int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dtype,
@@ -1316,14 +1355,18 @@ int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dty
         const size_t parts = (size_t)a.N * z.qblocks * z.max_chunks * a.Hq;
         a.max_chunks = c.max_chunks;
         a.chunk_tiles = c.chunk_tiles;
-        a.part_lse = reinterpret_cast<float*>(workspace);
-        a.part_o = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + parts * BQ * sizeof(float));
+        char* base = reinterpret_cast<char*>(workspace);
+        a.plan_flag = reinterpret_cast<int*>(base);
+        a.part_lse = reinterpret_cast<float*>(base + kPlanHeaderBytes);
+        a.part_o = reinterpret_cast<float*>(base + kPlanHeaderBytes + parts * BQ * sizeof(float));
     } else {   // no split, or no (or too small a) workspace: one chunk per unit
         a.max_chunks = 1;
         a.chunk_tiles = 1 << 30;
         a.part_lse = nullptr;
         a.part_o = nullptr;
+        a.plan_flag = nullptr;
     }
+    a.n_cus = device_cus();
     a.groups = a.N * a.qblocks * a.max_chunks * a.Hkv;
     const int G = a.Hq / a.Hkv;
     dim3 grid((unsigned)(((a.groups + kXcds - 1) / kXcds) * kXcds * G));

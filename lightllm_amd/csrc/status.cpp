@@ -22,6 +22,21 @@ int set_error(int status, const char* fmt, ...) {
     return status;
 }
 
+int device_cus() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    cache[dev] = cus;
+    return cus;
+}
+
 int resident_workgroups(const void* fn, int threads) {
     static std::mutex mu;
     static std::map<std::pair<int, const void*>, int> cache;

@@ -145,14 +145,15 @@ def test_prefill_workspace_size():
     assert ws(8, 4096, 512, 900, 14, 64, 16, 1) == 0
     # enough (sequence, query block, head) units to fill the GPU unsplit: no workspace
     assert ws(64, 32768, 512, 4608, 14, 64, 16, 1) == 0
-    # configuration 4 (keys up to 4608): chunked; per partial row an fp32 log-sum-exp and D
-    # fp16 values (fp16 pools)
+    # configuration 4 (keys up to 4608): chunked; a 256-byte header (the main kernel's
+    # split decision), then per partial row an fp32 log-sum-exp and D fp16 values (fp16 pools)
+    hdr = 256
     n = ws(8, 4096, 512, 4608, 14, 64, 16, 1)
-    assert n > 0 and n % (128 * (4 + 64 * 2)) == 0
+    assert n > hdr and (n - hdr) % (128 * (4 + 64 * 2)) == 0
     # fp32 and bf16 pools take the same plan with fp32 partial rows
     n32 = ws(8, 4096, 512, 4608, 14, 64, 16, 0)
-    assert n32 % (128 * (4 + 64 * 4)) == 0
-    assert n32 // (128 * 260) == n // (128 * 132)
+    assert (n32 - hdr) % (128 * (4 + 64 * 4)) == 0
+    assert (n32 - hdr) // (128 * 260) == (n - hdr) // (128 * 132)
     assert ws(8, 4096, 512, 4608, 14, 64, 16, 2) == n32
     # shapes outside the MFMA kernels (head_dim 67, page size 8) run unsplit: no workspace
     assert ws(8, 4096, 512, 4608, 14, 67, 16, 0) == 0

@@ -645,6 +645,12 @@ PREFILL = [
     ("fp32_mha", 4, 4, 64, [31], [97], torch.float32, True),
     ("fp32_D64_long", 14, 2, 64, [2500, 0], [300, 40], torch.float32, True),
     ("fp32_D128_long", 32, 8, 128, [2100], [130], torch.float32, True),
+    # the host plans a key split, and the kernel drops it because no unit is longer than a
+    # compute unit's share of the launch (the first N x qblocks work-groups take the units
+    # whole; the merge kernel sees the flag and writes nothing)
+    ("fp16_even_units_device_unsplit", 14, 2, 64, [0] * 4, [2048] * 4, torch.float16, True),
+    ("fp16_D128_even_device_unsplit", 32, 8, 128, [1024] * 16, [128] * 16, torch.float16, True),
+    ("fp32_even_device_unsplit", 14, 2, 64, [1024] * 8, [512] * 8, torch.float32, True),
     # head_dim 256 (Gemma-2 / Gemma-3 heads) on the MFMA kernels
     ("fp16_D256", 16, 8, 256, [0, 300], [200, 77], torch.float16, True),
     ("bf16_D256_long_noncausal", 8, 4, 256, [2200], [90], torch.bfloat16, False),
