@@ -910,6 +910,62 @@ def test_random_shapes(seed):
     _check(out, oracle_prefill(pc, kp, vp), dtype, f"random prefill {seed}")
 
 
+@pytest.mark.parametrize("seed", list(range(8)))
+def test_random_schedules(seed):
+    """Seeded shapes aimed at the automatic schedules rather than the head layouts: decode over
+    many short sequences (one split per unit), mid-size batches (the 16-wave unit kernel or the
+    balanced schedule), few long sequences (fixed splits + merge) and lognormal lengths
+    (balanced); prefill over cached prefixes of up to 4096 keys (key chunks, the device-side
+    split decision and the merge kernel) with ragged chunks, all three pool types."""
+    rng = np.random.default_rng(5000 + seed)
+    dtype = [torch.float32, torch.float16, torch.bfloat16][seed % 3]
+    hq, hkv, d = [(14, 2, 64), (32, 8, 128), (8, 1, 64), (16, 2, 128), (12, 4, 64)][seed % 5]
+    mode = seed % 4
+    if mode == 0:     # many short sequences
+        B = int(rng.integers(200, 1025))
+        lengths = rng.integers(16, 257, B)
+    elif mode == 1:   # mid-size batch, mid contexts
+        B = int(rng.integers(32, 201))
+        lengths = rng.integers(256, 1025, B)
+    elif mode == 2:   # few long sequences
+        B = int(rng.integers(1, 17))
+        lengths = rng.integers(2048, 8193, B)
+    else:             # uneven (lognormal) contexts
+        B = int(rng.integers(64, 257))
+        lengths = np.clip(rng.lognormal(np.log(512), 1.0, B), 1, 4096).astype(int)
+    # keep the oracle's work to a few seconds: at most ~12M cached (token, kv head, dim) values
+    cap = 12_000_000 // (hkv * d)
+    if int(lengths.sum()) > cap:
+        lengths = np.maximum(1, (lengths * (cap / lengths.sum())).astype(int))
+    lengths = [int(x) for x in lengths]
+    say(f"schedules {seed}: decode {dtype} {hq}/{hkv}/{d} B={B} max L={max(lengths)} "
+        f"sum L={sum(lengths)}")
+    need = sum((L + 1 + 15) // 16 for L in lengths)
+    case = wl.decode_case(f"sch{seed}", B, hq, hkv, d, lengths, need + 8, dtype, seed=seed)
+    out, kp, vp = run_decode(case)
+    _check(out, oracle_decode(case, np_pool(kp), np_pool(vp), threads=16), dtype, f"schedules decode {seed}")
+
+    n = int(rng.integers(1, 9))
+    prefixes = [int(x) for x in rng.integers(0, 4097, n)]
+    if seed % 2 == 0:   # even prefixes: the device may drop the planned split
+        prefixes = [prefixes[0]] * n
+    chunks = [int(x) for x in rng.integers(1, 769, n)]
+    # at most ~1.2e10 multiply-adds for the oracle
+    work = sum(c * (p_ + c) for p_, c in zip(prefixes, chunks)) * hq * d * 2
+    if work > 1.2e10:
+        f = (1.2e10 / work) ** 0.5
+        prefixes = [int(p_ * f) for p_ in prefixes]
+        chunks = [max(1, int(c * f)) for c in chunks]
+    causal = seed % 4 != 3
+    say(f"schedules {seed}: prefill {dtype} {hq}/{hkv}/{d} prefixes={prefixes} chunks={chunks} "
+        f"causal={causal}")
+    nb = sum((p_ + c_ + 15) // 16 for p_, c_ in zip(prefixes, chunks)) + 4
+    pc = wl.prefill_case(f"schp{seed}", hq, hkv, d, prefixes, chunks, {}, nb, dtype, seed=seed,
+                         causal=causal)
+    out, kp, vp = run_prefill(pc)
+    _check(out, oracle_prefill(pc, kp, vp), dtype, f"schedules prefill {seed}")
+
+
 # ---------------------------------------------------------------------------
 # C++ API (reference signatures) on the GPU
 # ---------------------------------------------------------------------------
