@@ -364,6 +364,11 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
     const int g = lane >> 4, c16 = lane & 15;
     Work wk;
     if (!take_work(a, sm.order, wk)) return;
+    // The ranking's arrays overlay the tile buffers.  Paged launches pass an
+    // LDS barrier (stage_pages) before the first tile is written; contiguous
+    // K/V has no page window, so every wave's reads of its unit from the
+    // ranking must complete here before any wave writes the first tile.
+    if constexpr (CG) lds_barrier();
     poison_uncovered_rows<T, D>(a, wk);
     const int hq = wk.hq, kvh = wk.kvh, unit = wk.unit, n = wk.n, ci = wk.ci;
     const int q0 = wk.q0, P = wk.P, q_lo = wk.q_lo, L = wk.L, kend = wk.kend;
@@ -851,6 +856,11 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
     const int g = lane >> 4, c16 = lane & 15;
     Work wk;
     if (!take_work(a, sm.order, wk)) return;
+    // The ranking's arrays overlay the tile buffers.  Paged launches pass an
+    // LDS barrier (stage_pages) before the first tile is written; contiguous
+    // K/V has no page window, so every wave's reads of its unit from the
+    // ranking must complete here before any wave writes the first tile.
+    if constexpr (CG) lds_barrier();
     poison_uncovered_rows<float, D>(a, wk);
     const int hq = wk.hq, kvh = wk.kvh, unit = wk.unit, n = wk.n, ci = wk.ci;
     const int q0 = wk.q0, P = wk.P, q_lo = wk.q_lo, L = wk.L, kend = wk.kend;

@@ -819,6 +819,11 @@ FIRST = [
     ("fp32_generic_D67", 4, 2, 67, [33, 100], [0, 2], torch.float32, False),
     ("fp16_D256", 16, 8, 256, [300, 41], [0, 5], torch.float16, True),
     ("fp32_D96_mha", 8, 8, 96, [300, 41, 129], [0, 5, 2], torch.float32, True),
+    # more work-groups than resident slots, with the longest-first ranking in LDS: work-groups that
+    # start late must read their unit before any wave of theirs stages the first tile over the ranking
+    ("fp32_16x512_second_wave", 14, 2, 64, [512] * 16, [0] * 16, torch.float32, True),
+    ("fp16_24x512_second_wave", 14, 2, 64, [512] * 24, [0] * 24, torch.float16, True),
+    ("bf16_12x512_D128_second_wave", 16, 2, 128, [512] * 12, [0] * 12, torch.bfloat16, True),
     # more than 1024 (entry, query block) units: index order instead of the longest-first ranking
     ("fp16_1200_units", 4, 2, 64, [(37 * i) % 250 + 1 for i in range(600)], [0] * 600, torch.float16,
      True),
