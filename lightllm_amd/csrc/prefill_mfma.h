@@ -65,6 +65,7 @@ struct MfmaPrefillArgs {
     // plan_flag (workspace header) receives 1 when the launch runs unsplit after all.
     int* plan_flag;
     int n_cus;        // compute units of the device
+    int resident;     // resident work-groups of the launched kernel
 };
 
 // Workspace bytes for the chunked schedule (0: the shape runs unchunked).

@@ -199,6 +199,9 @@ constexpr int kPageWindow = 256;   // page ids staged in LDS at a time
 #ifndef LLKV_PREFILL_XCD
 #define LLKV_PREFILL_XCD 1
 #endif
+#ifndef LLKV_PREFILL_REV
+#define LLKV_PREFILL_REV 1
+#endif
 constexpr int kXcds = 8;   // XCDs of an MI355X; work-groups go to them round-robin
 
 
@@ -220,17 +223,28 @@ struct Work {
 // it may return before or after the ranking barriers, never between).
 __device__ inline bool take_work(const MfmaPrefillArgs& a, int* order, Work& wk) {
     const int G = a.Hq / a.Hkv;
+    // Work-groups b, b + CUs, b + 2 CUs of the first resident set share a CU.
+    // When a CU holds two or more, the second set takes its items in reverse,
+    // so that the CU holding the longest item of the first set gets the
+    // shortest of the second.
+    int bid = blockIdx.x;
+#if LLKV_PREFILL_REV
+    if (a.resident >= 2 * a.n_cus && bid >= a.n_cus && bid < 2 * a.n_cus) {
+        const int hi = min(2 * a.n_cus, (int)gridDim.x);
+        bid = a.n_cus + (hi - 1 - bid);
+    }
+#endif
 #if LLKV_PREFILL_XCD
-    const int xcd = blockIdx.x % kXcds, r = blockIdx.x / kXcds;
+    const int xcd = bid % kXcds, r = bid / kXcds;
     const int j = (r / G) * kXcds + xcd;
     if (j >= a.groups) return false;
     wk.kvh = j % a.Hkv;
     wk.hq = wk.kvh * G + r % G;
     const int y = j / a.Hkv;
 #else
-    wk.hq = blockIdx.x % a.Hq;
+    wk.hq = bid % a.Hq;
     wk.kvh = wk.hq / G;
-    const int y = blockIdx.x / a.Hq;
+    const int y = bid / a.Hq;
     if (y * a.Hkv >= a.groups) return false;
 #endif
     // Every work-group takes the same decision from the same lengths.  Unsplit,
@@ -1377,6 +1391,8 @@ int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dty
         a.plan_flag = nullptr;
     }
     a.n_cus = device_cus();
+    a.resident = a.contig ? resident_workgroups(reinterpret_cast<const void*>(prefill_kernel(dtype, head_dim, true)), 256)
+                          : slots;
     a.groups = a.N * a.qblocks * a.max_chunks * a.Hkv;
     const int G = a.Hq / a.Hkv;
     dim3 grid((unsigned)(((a.groups + kXcds - 1) / kXcds) * kXcds * G));
