@@ -188,6 +188,7 @@ def bench_decode(args, torch, kc, wl):
         "decode_bytes": dec_bytes, "decode_bytes_pages": dec_bytes_pages, "append_bytes": app_bytes,
         "pool_bytes": 2 * kps[0].numel() * kps[0].element_size(),
         "parity_ok": ok, "max_abs_err": float(err.max()),
+        "schedule": kc.decode_schedule(B, hq, hkv, d, max_len, torch.float32),
     }
 
 
@@ -722,9 +723,11 @@ def main():
         "decode_GBps_page_granular": round(dec["decode_bytes_pages"] / (dec["decode_us_mean"] * 1e-6) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "llkv_paged_decode (automatic schedule for this batch: "
-                               "decode_split_kernel<MfmaDecode<float,64,7>> S=10, then "
-                               "decode_merge_kernel<float,1>)",
+                     "kernel": "llkv_paged_decode (automatic schedule for this batch, from "
+                               "llkv_paged_decode_schedule: %s, S=%d; %s)" % (
+                                   dec["schedule"][0], dec["schedule"][1],
+                                   "decode_split_kernel<MfmaDecode<float,64,7>> then decode_merge_kernel<float,1>"
+                                   if dec["schedule"][0] == "splits" else "the kernels of that schedule"),
                      "bytes_per_launch": dec["decode_bytes"],
                      "timing": "HIP events on the launch stream around a HIP-graph replay of "
                                f"--steps llkv_paged_decode calls ({args.layers} layer pools rotated, "

@@ -178,6 +178,25 @@ int llkv_paged_decode(void* out, const void* q, const void* k_pool,
                       float scale, int dtype, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* The schedule llkv_paged_decode (with_append 0) or llkv_paged_decode_append
+ * (with_append 1) takes for these shape arguments, for 16-byte aligned
+ * pointers on the current device: *kind is one of llkv_decode_schedule and
+ * *splits the key splits per (sequence, kv head) (0 for the balanced
+ * schedule).  No counterpart in the reference: it lets a caller see which
+ * kernels a batch shape runs (and what its workspace holds) without running it.
+ * Returns LLKV_OK or LLKV_ERR_INVALID. */
+enum llkv_decode_schedule {
+    LLKV_SCHED_ONE_SPLIT = 0,   /* one 4-wave work-group per (sequence, kv head), no merge */
+    LLKV_SCHED_UNIT = 1,        /* one 16-wave work-group per (sequence, kv head), no merge */
+    LLKV_SCHED_SPLITS = 2,      /* fixed key splits, then the log-sum-exp merge kernel      */
+    LLKV_SCHED_BALANCED = 3,    /* equal page shares per work-group, then the merge kernel  */
+    LLKV_SCHED_GENERIC = 4      /* shapes outside the tuned kernels (splits > 1: + merge)   */
+};
+int llkv_paged_decode_schedule(int num_seqs, int num_q_heads, int num_kv_heads,
+                               int head_dim, int block_size, int max_seq_len,
+                               int num_splits, int dtype, int with_append,
+                               int* kind, int* splits);
+
 /* Paged decode that allocates nothing and takes no workspace: llkv_paged_decode
  * with its split partials in a device array of the library
  * (llkv_paged_decode_noalloc_max_bytes() = 16 MiB per GPU, held until the

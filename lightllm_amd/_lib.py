@@ -48,6 +48,7 @@ _SIGS = {
                                   c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int,
                                   c_void_p, c_size_t, c_void_p]),
     "llkv_paged_decode_noalloc_max_bytes": (c_size_t, []),
+    "llkv_paged_decode_schedule": (c_int, [c_int] * 9 + [POINTER(c_int), POINTER(c_int)]),
     "llkv_paged_decode_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                           c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                           c_float, c_int, c_void_p]),

@@ -450,6 +450,23 @@ __global__ __launch_bounds__(64) void append_new_rows_kernel(DecodeArgs a) {
     }
 }
 
+// The schedule of a call: balanced, or fixed splits (num_splits updated to
+// the automatic choice) with wide = the 16-wave unit kernel for one split.
+void decide_schedule(const Kernels& ks, int num_seqs, int num_kv_heads, int block_size, int max_seq_len,
+                     int& num_splits, bool& balanced, bool& wide) {
+    const int max_pages_hint = (max_seq_len + block_size - 1) / block_size;
+    balanced = false;
+    wide = false;
+    if (num_splits == 0 && ks.split != nullptr) {
+        const AutoChoice c = auto_schedule(ks, num_seqs, num_kv_heads, max_pages_hint);
+        balanced = c.balanced;
+        wide = c.wide;
+        if (!balanced) num_splits = c.splits;
+    } else if (num_splits == 1 && ks.split != nullptr) {
+        wide = unit_schedule(ks, num_seqs, num_kv_heads, max_pages_hint);
+    }
+}
+
 int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_new,
                       const void* v_new, const void* k_pool, const void* v_pool,
                       const int* block_table, const int* seq_lens, int num_seqs, int num_q_heads,
@@ -487,14 +504,7 @@ int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_ne
     }
     const int max_pages_hint = (max_seq_len + block_size - 1) / block_size;
     bool balanced = false, wide = false;
-    if (num_splits == 0 && ks.split != nullptr) {
-        const AutoChoice c = auto_schedule(ks, num_seqs, num_kv_heads, max_pages_hint);
-        balanced = c.balanced;
-        wide = c.wide;
-        if (!balanced) num_splits = c.splits;
-    } else if (num_splits == 1 && ks.split != nullptr) {
-        wide = unit_schedule(ks, num_seqs, num_kv_heads, max_pages_hint);
-    }
+    decide_schedule(ks, num_seqs, num_kv_heads, block_size, max_seq_len, num_splits, balanced, wide);
 
     DecodeArgs a;
     a.out = out;
@@ -586,6 +596,35 @@ extern "C" int llkv_paged_decode(void* out, const void* q, const void* k_pool,
                              block_table, seq_lens, num_seqs, num_q_heads, num_kv_heads, head_dim,
                              block_size, max_blocks_per_seq, max_seq_len, num_splits, scale, dtype,
                              workspace, workspace_bytes, stream);
+}
+
+extern "C" int llkv_paged_decode_schedule(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                                          int block_size, int max_seq_len, int num_splits, int dtype,
+                                          int with_append, int* kind, int* splits) {
+    using namespace llkv;
+    const char* fn = "llkv_paged_decode_schedule";
+    if (!kind || !splits) return set_error(LLKV_ERR_INVALID, "%s: null pointer", fn);
+    if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+        num_splits < 0 || num_q_heads % num_kv_heads != 0 || dtype_bytes(dtype) == 0)
+        return set_error(LLKV_ERR_INVALID, "%s: bad shape arguments", fn);
+    if (max_seq_len < 0) max_seq_len = 0;
+    Kernels ks;
+    const size_t es = dtype_bytes(dtype);
+    if (block_size == kPage && ((size_t)num_kv_heads * head_dim * es) % 16 == 0 && head_dim <= 256)
+        ks = pick_tuned(dtype, head_dim, num_q_heads / num_kv_heads, with_append != 0);
+    bool balanced = false, wide = false;
+    decide_schedule(ks, num_seqs, num_kv_heads, block_size, max_seq_len, num_splits, balanced, wide);
+    if (balanced) {
+        *kind = LLKV_SCHED_BALANCED;
+        *splits = 0;
+        return LLKV_OK;
+    }
+    const Plan p = make_plan(block_size, max_seq_len, num_splits);
+    *splits = p.S_max;
+    if (ks.split == nullptr) *kind = LLKV_SCHED_GENERIC;
+    else if (p.S_max > 1) *kind = LLKV_SCHED_SPLITS;
+    else *kind = wide ? LLKV_SCHED_UNIT : LLKV_SCHED_ONE_SPLIT;
+    return LLKV_OK;
 }
 
 extern "C" int llkv_paged_decode_append(void* out, const void* q, const void* k_new,

@@ -32,6 +32,7 @@ def _decode_setup(name, B, hq, hkv, d, lengths, dtype, seed):
     def run(o):
         kc.append_kv(kn, vn, slots, kp, vp)
         kc.paged_decode(q, kp, vp, bt, sl, c.max_seq_len, out=o, workspace=ws)
+    run.schedule = kc.decode_schedule(B, hq, hkv, d, c.max_seq_len, dtype)[0]
     return q, out, run
 
 
@@ -62,7 +63,7 @@ def test_graph_replays_match_eager():
         # few long sequences: fixed splits + merge kernel
         ("split", _decode_setup("g_split", 4, 14, 2, 64, [6000, 3000, 9000, 100], torch.float32, 2)),
         # mid-size batch of mid contexts: 16-wave unit kernel
-        ("unit", _decode_setup("g_unit", 40, 32, 8, 128, [900] * 40, torch.float16, 3)),
+        ("unit", _decode_setup("g_unit", 24, 32, 8, 128, [700] * 24, torch.float16, 3)),
         # many short sequences: one split per unit on 4-wave work-groups
         ("onesplit", _decode_setup("g_one", 512, 14, 2, 64, [100] * 512, torch.bfloat16, 4)),
         # uneven cached prefixes: key chunks + merge kernel
@@ -71,6 +72,11 @@ def test_graph_replays_match_eager():
         # even prefixes: the device drops the planned split, the merge kernel returns
         ("prefill_even", _prefill_setup("g_pfe", 14, 2, 64, [2048] * 2, [2048] * 2, torch.float16, 6)),
     ]
+    # each decode setup runs the schedule it is named for
+    for name, (q, out, run) in setups:
+        if hasattr(run, "schedule"):
+            say(f"{name}: schedule {run.schedule}")
+            assert run.schedule == {"split": "splits", "onesplit": "one_split"}.get(name, name)
     # eager warm-up (library load, workspace first touch)
     for _, (q, out, run) in setups:
         run(out)

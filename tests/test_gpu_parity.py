@@ -553,6 +553,26 @@ def test_decode_auto_schedule_shapes(name, lengths, hint, dtype):
             assert torch.count_nonzero(out[b]).item() == 0
 
 
+def test_decode_schedule_query():
+    """llkv_paged_decode_schedule reports the automatic choice for the benchmark configurations and
+    the schedule rules (16-byte aligned operands, one MI355X)."""
+    q = kc.decode_schedule
+    assert q(1, 14, 2, 64, 513, torch.float32) == ("splits", 9)          # configuration 1
+    assert q(64, 14, 2, 64, 2049, torch.float32) == ("splits", 10)       # configuration 2
+    name, s = q(16, 14, 2, 64, 32768, torch.float16)                     # configuration 3
+    assert name == "splits" and s > 16
+    assert q(256, 32, 8, 128, 16385, torch.float16)[0] == "balanced"     # configuration 5 decode
+    assert q(512, 14, 2, 64, 101, torch.bfloat16) == ("one_split", 1)    # <= 8 pages
+    assert q(24, 32, 8, 128, 701, torch.float16) == ("unit", 1)          # 16-wave work-groups
+    assert q(4, 14, 2, 64, 2049, torch.float32, num_splits=4) == ("splits", 4)
+    assert q(4, 14, 2, 64, 2049, torch.float32, num_splits=1) == ("one_split", 1)
+    assert q(4, 10, 1, 64, 2049, torch.float32)[0] == "generic"          # G = 10: generic body
+    assert q(4, 14, 2, 67, 2049, torch.float32)[0] == "generic"          # head_dim 67
+    assert q(4, 14, 2, 64, 2049, torch.float32, block_size=8)[0] == "generic"
+    with pytest.raises(Exception, match="bad shape"):
+        q(4, 14, 3, 64, 2049, torch.float32)                             # Hq not a multiple of Hkv
+
+
 def test_decode_noncontiguous_table_and_empty():
     say("decode: table [7,3,11], zero-length sequence in a batch")
     g = torch.Generator().manual_seed(13)
