@@ -251,8 +251,8 @@ int llkv_paged_decode_append(void* out, const void* q, const void* k_new,
  *             reference kernel (src/kv_cache/paged_attention.cu:658,712).
  * max_q_len, max_seq_len: host-side upper bounds (grid sizing).
  * workspace : device memory of llkv_paged_prefill_workspace_size() bytes for
- *             the partials of long key ranges (fp16 rows for fp16 pools,
- *             fp32 otherwise; fp32 log-sum-exp), which are then cut into
+ *             the partials of long key ranges (fp32 rows and log-sum-exp),
+ *             which are then cut into
  *             chunks run in parallel; NULL (or a size of 0) runs every key
  *             range unsplit.  Calls sharing one workspace must not overlap.
  * ------------------------------------------------------------------------ */

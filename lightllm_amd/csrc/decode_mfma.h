@@ -75,16 +75,23 @@ template <int D> struct ScoreOps<float, D> {
 #pragma unroll
         for (int cc = 0; cc < NK; ++cc) k[cc] = *reinterpret_cast<const float4*>(krow + 16 * cc + 4 * g);
     }
+    // From head_dim 128 on, the two halves of the head dims accumulate apart
+    // and are added at the end: half the rounding steps in each sum, which
+    // halves the score's rounding error (it dominates the fp32 output's error
+    // there).  At head_dim 64 the second accumulator would spill registers in
+    // the fused-append variant.
     __device__ static mf32x4 scores(const KReg (&k)[NK], const QReg (&q)[NQ], float) {
-        mf32x4 s = {0.f, 0.f, 0.f, 0.f};
+        constexpr int kHalf = D >= 128 ? NK / 2 : NK;
+        mf32x4 s = {0.f, 0.f, 0.f, 0.f}, t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int cc = 0; cc < NK; ++cc) {
-            s = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].x, q[4 * cc + 0], s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].y, q[4 * cc + 1], s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].z, q[4 * cc + 2], s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].w, q[4 * cc + 3], s, 0, 0, 0);
+            mf32x4& acc = cc < kHalf ? s : t;
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].x, q[4 * cc + 0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].y, q[4 * cc + 1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].z, q[4 * cc + 2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].w, q[4 * cc + 3], acc, 0, 0, 0);
         }
-        return s;   // Q was pre-scaled
+        return s + t;   // Q was pre-scaled
     }
     // V[row][dims 4c .. 4c+3] widened to fp32
     __device__ static float4 load_v4(const float* p) { return *reinterpret_cast<const float4*>(p); }

@@ -23,8 +23,8 @@
 // When the units alone would not fill the GPU, key ranges are cut into chunks
 // of chunk_tiles tiles, one work-group each (N x qblocks x max_chunks x Hq
 // work-groups, the q heads of one kv head on one XCD), so that a cached prefix of thousands of keys does not
-// serialise on one work-group; their partials (normalised rows, fp16 for
-// fp16 pools and fp32 otherwise, + fp32 log2-sum-exp2) are merged by
+// serialise on one work-group; their partials (normalised fp32 rows + fp32
+// log2-sum-exp2) are merged by
 // prefill_merge_kernel.  The host plans the split from the shape bounds and the
 // kernel's resident work-group count; the kernel then drops it when the units'
 // actual key lengths are even enough (no unit longer than the average load of
@@ -59,7 +59,7 @@ struct MfmaPrefillArgs {
     int max_chunks;   // key chunks per (sequence, query block)
     int chunk_tiles;  // key tiles per chunk
     int groups;       // N * qblocks * max_chunks * Hkv (chunk slot, kv head) work items
-    float* part_o;    // [N*qblocks*max_chunks*Hq][BQ][D] (max_chunks > 1), fp16 elements for fp16 pools
+    float* part_o;    // [N*qblocks*max_chunks*Hq][BQ][D] (max_chunks > 1)
     float* part_lse;  // [N*qblocks*max_chunks*Hq][BQ]
     // Split decision made on the device from the units' key lengths (max_chunks > 1):
     // plan_flag (workspace header) receives 1 when the launch runs unsplit after all.

@@ -41,14 +41,10 @@ template <> struct Mfma<bf16_t> {
 
 constexpr int BQ = 128;   // query rows per work-group
 
-// Key-chunk partial rows of fp16 pools are kept in fp16 (normalised rows,
-// |o| <= max |v|; half the merge's traffic); bf16 and fp32 pools keep fp32
-// partials (bf16 values can exceed the fp16 range).
-#ifndef LLKV_PF_HALF_PARTIALS
-#define LLKV_PF_HALF_PARTIALS 1
-#endif
-template <typename T> struct HalfParts { static constexpr bool value = false; };
-template <> struct HalfParts<_Float16> { static constexpr bool value = LLKV_PF_HALF_PARTIALS != 0; };
+// Key-chunk partial rows are fp32 for every pool type.  fp16 rows (half the
+// merge's traffic, 2-3 us on configuration 4) added a rounding of each chunk's
+// normalised row, which chunks of opposite sign amplify in the merged output:
+// seeded ragged batches over 4k-key prefixes went past the fp16 bound.
 constexpr int WQ = 32;    // query rows per wave (two 16-column MFMA tiles)
 constexpr int BN = 64;    // keys per tile (four pages)
 
@@ -773,16 +769,6 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 w2.y = Mfma<T>::pack2(o[dt][nt][2] * inv, o[dt][nt][3] * inv);
                 *reinterpret_cast<uint2*>(orow + dt * 16 + 4 * g) = w2;
             }
-        } else if constexpr (HalfParts<T>::value) {
-            _Float16* prow = reinterpret_cast<_Float16*>(a.part_o) + (pidx * BQ + row) * D;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                uint2 w2;
-                w2.x = pack_h2(o[dt][nt][0] * inv, o[dt][nt][1] * inv);
-                w2.y = pack_h2(o[dt][nt][2] * inv, o[dt][nt][3] * inv);
-                *reinterpret_cast<uint2*>(prow + dt * 16 + 4 * g) = w2;
-            }
-            if (g == 0) a.part_lse[pidx * BQ + row] = lt > 0.f ? m[nt] + fast_log2(lt) : -INFINITY;
         } else {
             float* prow = a.part_o + (pidx * BQ + row) * D;
 #pragma unroll
@@ -1200,37 +1186,22 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(MfmaPrefillArgs a) {
     // the row loads behind the lse.  A chunk whose row saw no key has lse -inf
     // and a zero row: weight 0, no change.
     constexpr int CB = D <= 64 ? 4 : 2;
-    constexpr int NR = HalfParts<T>::value ? V4 / 2 : V4;   // 16-byte loads per chunk row slice
     for (int c0 = 0; c0 < nchunks; c0 += CB) {
         float l[CB];
-        uint4 raw[CB][NR];
+        float4 raw[CB][V4];
 #pragma unroll
         for (int k = 0; k < CB; ++k) {
             const int c = min(c0 + k, nchunks - 1);
             const int64_t pc = (p0 + (int64_t)c * a.Hq) * BQ + row;
             const float lk = a.part_lse[pc];
             l[k] = c0 + k < nchunks ? lk : -INFINITY;
-            const uint4* src = HalfParts<T>::value
-                                   ? reinterpret_cast<const uint4*>(reinterpret_cast<const _Float16*>(a.part_o) + pc * D) + part * NR
-                                   : reinterpret_cast<const uint4*>(a.part_o + pc * D) + part * NR;
+            const float4* src = reinterpret_cast<const float4*>(a.part_o + pc * D) + part * V4;
 #pragma unroll
-            for (int v = 0; v < NR; ++v) raw[k][v] = src[v];
+            for (int v = 0; v < V4; ++v) raw[k][v] = src[v];
         }
 #pragma unroll
         for (int k = 0; k < CB; ++k) {
-            float4 o[V4];
-            if constexpr (HalfParts<T>::value) {
-#pragma unroll
-                for (int v = 0; v < NR; ++v) {
-                    float f[8];
-                    Chunk<_Float16>::unpack(raw[k][v], f);
-                    o[2 * v] = make_float4(f[0], f[1], f[2], f[3]);
-                    o[2 * v + 1] = make_float4(f[4], f[5], f[6], f[7]);
-                }
-            } else {
-#pragma unroll
-                for (int v = 0; v < V4; ++v) o[v] = __builtin_bit_cast(float4, raw[k][v]);
-            }
+            const float4* o = raw[k];
             const float Mn = fmaxf(M, l[k]);
             const bool live = Mn != -INFINITY;   // some key seen by this row so far
             const float sc = live ? fast_exp2(M - Mn) : 1.0f;
@@ -1359,8 +1330,7 @@ size_t prefill_mfma_workspace(int N, int Hq, int head_dim, int block_size, int d
     const ChunkPlan c = chunk_plan(N, Hq, total_q, max_q_len, max_seq_len, 0);
     if (c.max_chunks <= 1) return 0;
     const size_t parts = (size_t)N * c.qblocks * c.max_chunks * Hq;
-    const size_t part_elem = (dtype == LLKV_DTYPE_F16 && HalfParts<_Float16>::value) ? 2 : sizeof(float);
-    return kPlanHeaderBytes + parts * BQ * sizeof(float) + parts * BQ * head_dim * part_elem;
+    return kPlanHeaderBytes + parts * BQ * sizeof(float) + parts * BQ * head_dim * sizeof(float);
 }
 
 int launch_prefill_mfma(MfmaPrefillArgs a, int head_dim, int block_size, int dtype,

@@ -146,22 +146,21 @@ def test_prefill_workspace_size():
     # enough (sequence, query block, head) units to fill the GPU unsplit: no workspace
     assert ws(64, 32768, 512, 4608, 14, 64, 16, 1) == 0
     # configuration 4 (keys up to 4608): chunked; a 256-byte header (the main kernel's
-    # split decision), then per partial row an fp32 log-sum-exp and D fp16 values (fp16 pools)
+    # split decision), then per partial row an fp32 log-sum-exp and D fp32 values
     hdr = 256
     n = ws(8, 4096, 512, 4608, 14, 64, 16, 1)
-    assert n > hdr and (n - hdr) % (128 * (4 + 64 * 2)) == 0
-    # fp32 and bf16 pools take the same plan with fp32 partial rows
+    assert n > hdr and (n - hdr) % (128 * (4 + 64 * 4)) == 0
+    # fp32 and bf16 pools take the same plan and the same partial rows
     n32 = ws(8, 4096, 512, 4608, 14, 64, 16, 0)
-    assert (n32 - hdr) % (128 * (4 + 64 * 4)) == 0
-    assert (n32 - hdr) // (128 * 260) == (n - hdr) // (128 * 132)
+    assert n32 == n
     assert ws(8, 4096, 512, 4608, 14, 64, 16, 2) == n32
     # shapes outside the MFMA kernels (head_dim 67, page size 8) run unsplit: no workspace
     assert ws(8, 4096, 512, 4608, 14, 67, 16, 0) == 0
     assert ws(8, 4096, 512, 4608, 14, 64, 8, 1) == 0
-    # head_dim 256 on the MFMA kernels: chunked, fp32 partial rows twice the fp16 ones
+    # head_dim 256 on the MFMA kernels: chunked, the same fp32 partial rows for every pool type
     n16 = ws(8, 4096, 512, 4608, 16, 256, 16, 1)
     n32 = ws(8, 4096, 512, 4608, 16, 256, 16, 0)
-    assert n16 > 0 and n32 > n16
+    assert n16 > 0 and n32 == n16 and (n16 - hdr) % (128 * (4 + 256 * 4)) == 0
 
 
 def test_hash_tokens_abi():
