@@ -901,7 +901,9 @@ def _check(out, ref, dtype, what):
         check_lowp(out, ref, what, 2e-3 if dtype == torch.float16 else 1.6e-2)
 
 
-@pytest.mark.parametrize("seed", list(range(16)))
+# 186: fp32 head_dim 256, G = 7 (the generic decode) at 0.80 of the bound while its score was one
+# running sum over the head dims
+@pytest.mark.parametrize("seed", list(range(16)) + [186])
 def test_random_shapes(seed):
     """Decode and prefill on seeded random shapes: group sizes 1-8, head_dim 64 / 128 / 256
     (decode) and 64 / 128 (prefill), 1-4 kv heads, ragged and empty lengths, fixed and
