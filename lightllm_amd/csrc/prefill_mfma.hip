@@ -1237,9 +1237,12 @@ bool prefill_mfma_handles(int head_dim, int block_size, int dtype) {
 // (k = 1) nothing is split: no partials and no merge.  The workspace is sized
 // from the shape alone, for kSizingSlots resident slots (256 CUs x 4
 // work-groups, above what this kernel reaches); a launch takes the smaller of
-// that k and the one of its device's actual resident count.
+// that k and the one of its device's actual resident count.  About one
+// work-group per slot: with fp32 partials, configuration 4 runs two chunks
+// per long unit at 58.1 us against 59.8 us for three (1.5 per slot) and
+// 80 us for two per slot; the fewer chunks, the less partial traffic.
 #ifndef LLKV_PREFILL_FILL
-#define LLKV_PREFILL_FILL 1.5
+#define LLKV_PREFILL_FILL 1.0
 #endif
 constexpr double kFill = LLKV_PREFILL_FILL;
 constexpr int kMinChunkTiles = 8;
