@@ -179,7 +179,8 @@ int llkv_paged_decode(void* out, const void* q, const void* k_pool,
                       size_t workspace_bytes, void* stream);
 
 /* The schedule llkv_paged_decode (with_append 0) or llkv_paged_decode_append
- * (with_append 1) takes for these shape arguments, for 16-byte aligned
+ * (with_append 1; it takes the plain call's schedule, so that its results equal
+ * append + decode bit for bit) takes for these shape arguments, for 16-byte aligned
  * pointers on the current device: *kind is one of llkv_decode_schedule and
  * *splits the key splits per (sequence, kv head) (0 for the balanced
  * schedule).  No counterpart in the reference: it lets a caller see which

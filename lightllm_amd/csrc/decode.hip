@@ -513,7 +513,11 @@ int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_ne
     }
     const int max_pages_hint = (max_seq_len + block_size - 1) / block_size;
     bool balanced = false, wide = false;
-    decide_schedule(ks, num_seqs, num_kv_heads, block_size, max_seq_len, num_splits, balanced, wide);
+    // The fused-append call takes the plain call's schedule (from the plain
+    // kernels' resident counts), so that its results equal append + decode
+    // bit for bit.
+    const Kernels sched = (k_new != nullptr && ks.split != nullptr) ? pick_tuned(dtype, head_dim, G, false) : ks;
+    decide_schedule(sched, num_seqs, num_kv_heads, block_size, max_seq_len, num_splits, balanced, wide);
 
     DecodeArgs a;
     a.out = out;
@@ -620,7 +624,8 @@ extern "C" int llkv_paged_decode_schedule(int num_seqs, int num_q_heads, int num
     Kernels ks;
     const size_t es = dtype_bytes(dtype);
     if (block_size == kPage && ((size_t)num_kv_heads * head_dim * es) % 16 == 0 && head_dim <= 256)
-        ks = pick_tuned(dtype, head_dim, num_q_heads / num_kv_heads, with_append != 0);
+        ks = pick_tuned(dtype, head_dim, num_q_heads / num_kv_heads, false);   // as the fused call
+    (void)with_append;
     bool balanced = false, wide = false;
     decide_schedule(ks, num_seqs, num_kv_heads, block_size, max_seq_len, num_splits, balanced, wide);
     if (balanced) {

@@ -47,6 +47,9 @@ typedef short ms16x4 __attribute__((ext_vector_type(4)));
 #ifndef LLKV_DECODE_HALF_PV
 #define LLKV_DECODE_HALF_PV 1
 #endif
+#ifndef LLKV_DECODE_A4
+#define LLKV_DECODE_A4 1
+#endif
 typedef __bf16 mbf16x8 __attribute__((ext_vector_type(8)));
 
 // Score operands S^T = K Q^T per element type.  load_q fills the Q^T operand
@@ -169,8 +172,14 @@ struct MfmaDecode {
     // registers) for head_dim 64; head_dim 128 needs more and gets 4.
     // head_dim 256: ~200 VGPRs (two waves per SIMD, no spills; three spill 33-49).
     // The unit schedule's 16-wave work-group puts four waves on each SIMD.
+    // The fused-append variant of fp32 pools holds one wave per SIMD fewer:
+    // its new-row pointers took it past the register budget (2-9 registers
+    // spilled at head_dim 64, ~50 at 128); configuration 2 fused 25.9 ->
+    // 24.5 us at four waves.
+    static constexpr bool kA32 = LLKV_DECODE_A4 && A && Elem<T>::kDtype == LLKV_DTYPE_F32;
     static constexpr int kWavesPerEU =
-        W > kDecodeWaves ? 4 : (D == 64 ? 5 : (D == 96 ? 3 : (D == 128 ? 4 : 2)));
+        W > kDecodeWaves ? 4
+                         : (D == 64 ? (kA32 ? 4 : 5) : (D == 96 ? 3 : (D == 128 ? (kA32 ? 3 : 4) : 2)));
     // Segments per round: two where the LDS for the parked states stays small.
     // (The unit schedule runs one segment per work-group.)
     static constexpr int kSegMax = (W == kDecodeWaves && G * D <= 512) ? 2 : 1;
