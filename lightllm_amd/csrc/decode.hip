@@ -545,7 +545,7 @@ int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_ne
         if (workspace == nullptr || workspace_bytes < w.total)
             return set_error(LLKV_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", fn,
                              workspace_bytes, w.total);
-        a.nwg = balanced_wgs(ks.balanced, (int64_t)num_seqs * num_kv_heads * max_pages_hint);
+        a.nwg = balanced_wgs(sched.balanced, (int64_t)num_seqs * num_kv_heads * max_pages_hint);   // as the plain call
         a.plan = reinterpret_cast<int*>(ws + w.plan_off);
         a.part_lse = reinterpret_cast<float*>(ws + w.lse_off);
         a.part_o = reinterpret_cast<float*>(ws + w.o_off);

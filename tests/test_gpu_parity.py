@@ -243,6 +243,10 @@ FUSED = [
     ("f32_G5_S3", 20, 10, 2, 64, torch.float32, 3, (1, 900)),
     ("f16_D256_G2_auto", 24, 16, 8, 256, torch.float16, 0, (1, 2500)),
     ("f32_D96_MHA_auto", 30, 8, 8, 96, torch.float32, 0, (1, 1200)),
+    # balanced schedule on fp32 pools, whose fused bodies hold fewer waves per SIMD than the plain
+    # ones: the fused call takes the plain call's work-group count
+    ("f32_G7_balanced", 400, 14, 2, 64, torch.float32, 0, (1, 3000)),
+    ("f32_llama_D128_balanced", 160, 32, 8, 128, torch.float32, 0, (1, 2000)),
     # the unit schedule (one 16-wave work-group per sequence and kv head, no merge)
     ("f32_G7_unit_auto", 64, 14, 2, 64, torch.float32, 0, (1, 250)),
     ("f16_llama_unit_auto", 32, 32, 8, 128, torch.float16, 0, (1, 256)),
