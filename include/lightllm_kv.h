@@ -188,7 +188,8 @@ int llkv_paged_decode(void* out, const void* q, const void* k_pool,
  * Returns LLKV_OK or LLKV_ERR_INVALID. */
 enum llkv_decode_schedule {
     LLKV_SCHED_ONE_SPLIT = 0,   /* one 4-wave work-group per (sequence, kv head), no merge */
-    LLKV_SCHED_UNIT = 1,        /* one 16-wave work-group per (sequence, kv head), no merge */
+    LLKV_SCHED_UNIT = 1,        /* 16-wave work-groups: one per (sequence, kv head), no merge,
+                                   or (splits > 1, long contexts) fixed splits + merge     */
     LLKV_SCHED_SPLITS = 2,      /* fixed key splits, then the log-sum-exp merge kernel      */
     LLKV_SCHED_BALANCED = 3,    /* equal page shares per work-group, then the merge kernel  */
     LLKV_SCHED_GENERIC = 4      /* shapes outside the tuned kernels (splits > 1: + merge)   */

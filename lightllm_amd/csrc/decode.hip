@@ -328,6 +328,9 @@ int balanced_wgs(DecodeFn fn, int64_t page_units_bound) {
 // pages; with many units (a large batch of uneven lengths) the balanced
 // schedule shares the pages equally instead.
 constexpr int kAutoMaxSplits = 64;
+#ifndef LLKV_DECODE_WIDE_SPLITS
+#define LLKV_DECODE_WIDE_SPLITS 1
+#endif
 constexpr int kShortChainPages = 4;   // pages per wave up to which a split is latency-bound
 
 struct AutoChoice {
@@ -389,7 +392,22 @@ AutoChoice auto_schedule(const Kernels& ks, int B, int Hkv, int max_pages) {
     // (latency-bound: every extra work-group adds loads in flight); 0.8 of it when
     // the chains are long (bandwidth-bound: extra work-groups only contend).
     int64_t S = (cap + units - 1) / units;
-    if ((int64_t)max_pages > S * kDecodeWaves * kShortChainPages) S = (cap * 4 / 5 + units - 1) / units;
+    if ((int64_t)max_pages > S * kDecodeWaves * kShortChainPages) {
+#if LLKV_DECODE_WIDE_SPLITS
+        // Long chains: the 16-wave kernel at 0.8 of its resident count, a
+        // quarter as many splits (and partials to merge) for the same waves.
+        if (ks.unit != nullptr) {
+            const int cap16 = resident_workgroups(reinterpret_cast<const void*>(ks.unit), 64 * kUnitWaves);
+            const int64_t S16 = std::min<int64_t>((cap16 * 4 / 5 + units - 1) / units, kAutoMaxSplits);
+            if (S16 > 1 && (int64_t)max_pages > S16 * kUnitWaves * kShortChainPages) {
+                c.wide = true;
+                c.splits = (int)S16;
+                return c;
+            }
+        }
+#endif
+        S = (cap * 4 / 5 + units - 1) / units;
+    }
     // at least one page per wave of a split (smaller splits only add partials to merge)
     const int64_t by_pages = (std::max(1, max_pages) + kDecodeWaves - 1) / kDecodeWaves;
     S = std::max<int64_t>(1, std::min<int64_t>({S, (int64_t)kAutoMaxSplits, by_pages}));
@@ -568,7 +586,7 @@ int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_ne
         a.fixed_S = p.fixed_S;
         if (ks.split) {
             dim3 grid(p.S_max, num_kv_heads, num_seqs);
-            if (wide && p.S_max == 1)   // the unit schedule's wider work-groups
+            if (wide)   // the 16-wave work-groups (one split, or long chains)
                 ks.unit<<<grid, 64 * kUnitWaves, 0, st>>>(a);
             else
                 ks.split<<<grid, 64 * kDecodeWaves, 0, st>>>(a);
@@ -636,8 +654,8 @@ extern "C" int llkv_paged_decode_schedule(int num_seqs, int num_q_heads, int num
     const Plan p = make_plan(block_size, max_seq_len, num_splits);
     *splits = p.S_max;
     if (ks.split == nullptr) *kind = LLKV_SCHED_GENERIC;
-    else if (p.S_max > 1) *kind = LLKV_SCHED_SPLITS;
-    else *kind = wide ? LLKV_SCHED_UNIT : LLKV_SCHED_ONE_SPLIT;
+    else if (wide) *kind = LLKV_SCHED_UNIT;
+    else *kind = p.S_max > 1 ? LLKV_SCHED_SPLITS : LLKV_SCHED_ONE_SPLIT;
     return LLKV_OK;
 }
 

@@ -258,8 +258,9 @@ DECODE_SCHEDULES = ("one_split", "unit", "splits", "balanced", "generic")
 def decode_schedule(num_seqs: int, hq: int, hkv: int, d: int, max_seq_len: int, dtype: torch.dtype,
                     num_splits: int = 0, block_size: int = 16, with_append: bool = False):
     """(schedule name, key splits) that paged_decode / paged_decode_append take for this shape on
-    the current device (llkv_paged_decode_schedule): one_split and unit run one kernel, splits
-    and balanced a merge kernel after it."""
+    the current device (llkv_paged_decode_schedule): one_split runs one kernel, unit one kernel
+    (splits == 1) or 16-wave splits and a merge kernel, splits and balanced a merge kernel after
+    the split kernel."""
     kind, splits = ctypes.c_int(), ctypes.c_int()
     check(lib().llkv_paged_decode_schedule(num_seqs, hq, hkv, d, block_size, max_seq_len, num_splits,
                                            dtype_code(dtype), int(with_append), ctypes.byref(kind),
