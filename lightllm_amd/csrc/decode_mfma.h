@@ -78,23 +78,28 @@ template <int D> struct ScoreOps<float, D> {
 #pragma unroll
         for (int cc = 0; cc < NK; ++cc) k[cc] = *reinterpret_cast<const float4*>(krow + 16 * cc + 4 * g);
     }
-    // From head_dim 128 on, the two halves of the head dims accumulate apart
-    // and are added at the end: half the rounding steps in each sum, which
-    // halves the score's rounding error (it dominates the fp32 output's error
-    // there).  At head_dim 64 the second accumulator would spill registers in
-    // the fused-append variant.
+    // From head_dim 128 on, the four quarters of the head dims accumulate
+    // apart and are added pairwise at the end: a quarter of the rounding steps
+    // in each sum (the score's rounding dominates the fp32 output's error
+    // there; one running sum reached the bound on seeded shapes, two sums
+    // 1.007 of it on one of ~600).  At head_dim 64 more accumulators would
+    // spill registers in the fused-append variant.
     __device__ static mf32x4 scores(const KReg (&k)[NK], const QReg (&q)[NQ], float) {
-        constexpr int kHalf = D >= 128 ? NK / 2 : NK;
-        mf32x4 s = {0.f, 0.f, 0.f, 0.f}, t = {0.f, 0.f, 0.f, 0.f};
+        constexpr int kParts = D >= 128 ? 4 : 1;   // running sums over consecutive dim blocks
+        constexpr int kPer = NK / kParts;
+        mf32x4 acc[kParts];
+#pragma unroll
+        for (int j = 0; j < kParts; ++j) acc[j] = mf32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int cc = 0; cc < NK; ++cc) {
-            mf32x4& acc = cc < kHalf ? s : t;
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].x, q[4 * cc + 0], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].y, q[4 * cc + 1], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].z, q[4 * cc + 2], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].w, q[4 * cc + 3], acc, 0, 0, 0);
+            mf32x4& a = acc[cc / kPer];
+            a = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].x, q[4 * cc + 0], a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].y, q[4 * cc + 1], a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].z, q[4 * cc + 2], a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x4f32(k[cc].w, q[4 * cc + 3], a, 0, 0, 0);
         }
-        return s + t;   // Q was pre-scaled
+        if constexpr (kParts == 1) return acc[0];   // Q was pre-scaled
+        else return (acc[0] + acc[1]) + (acc[2] + acc[3]);
     }
     // V[row][dims 4c .. 4c+3] widened to fp32
     __device__ static float4 load_v4(const float* p) { return *reinterpret_cast<const float4*>(p); }
