@@ -185,6 +185,9 @@ int llkv_paged_decode(void* out, const void* q, const void* k_pool,
  * *splits the key splits per (sequence, kv head) (0 for the balanced
  * schedule).  No counterpart in the reference: it lets a caller see which
  * kernels a batch shape runs (and what its workspace holds) without running it.
+ * The decode calls first clamp max_seq_len to max_blocks_per_seq * block_size;
+ * this query takes no table width, so it reports the call's schedule when
+ * max_seq_len is already within that bound (pass the clamped value otherwise).
  * Returns LLKV_OK or LLKV_ERR_INVALID. */
 enum llkv_decode_schedule {
     LLKV_SCHED_ONE_SPLIT = 0,   /* one 4-wave work-group per (sequence, kv head), no merge */

@@ -328,9 +328,6 @@ int balanced_wgs(DecodeFn fn, int64_t page_units_bound) {
 // pages; with many units (a large batch of uneven lengths) the balanced
 // schedule shares the pages equally instead.
 constexpr int kAutoMaxSplits = 64;
-#ifndef LLKV_DECODE_WIDE_SPLITS
-#define LLKV_DECODE_WIDE_SPLITS 1
-#endif
 constexpr int kShortChainPages = 4;   // pages per wave up to which a split is latency-bound
 
 struct AutoChoice {
@@ -393,7 +390,6 @@ AutoChoice auto_schedule(const Kernels& ks, int B, int Hkv, int max_pages) {
     // the chains are long (bandwidth-bound: extra work-groups only contend).
     int64_t S = (cap + units - 1) / units;
     if ((int64_t)max_pages > S * kDecodeWaves * kShortChainPages) {
-#if LLKV_DECODE_WIDE_SPLITS
         // Long chains: the 16-wave kernel at 0.8 of its resident count, a
         // quarter as many splits (and partials to merge) for the same waves.
         if (ks.unit != nullptr) {
@@ -405,7 +401,6 @@ AutoChoice auto_schedule(const Kernels& ks, int B, int Hkv, int max_pages) {
                 return c;
             }
         }
-#endif
         S = (cap * 4 / 5 + units - 1) / units;
     }
     // at least one page per wave of a split (smaller splits only add partials to merge)

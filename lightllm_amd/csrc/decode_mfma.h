@@ -44,12 +44,6 @@ typedef _Float16 mf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 mf16x4 __attribute__((ext_vector_type(4)));
 typedef short ms16x4 __attribute__((ext_vector_type(4)));
 
-#ifndef LLKV_DECODE_HALF_PV
-#define LLKV_DECODE_HALF_PV 1
-#endif
-#ifndef LLKV_DECODE_A4
-#define LLKV_DECODE_A4 1
-#endif
 typedef __bf16 mbf16x8 __attribute__((ext_vector_type(8)));
 
 // Score operands S^T = K Q^T per element type.  load_q fills the Q^T operand
@@ -172,7 +166,7 @@ struct MfmaDecode {
     // on a B = 64 Gemma-2 shape in fp16.  At head_dim 64 / 128 the page loop is
     // not bound by its MFMAs and this form measured 1-2 % slower, so those, and
     // fp32 pools, keep v_mfma_f32_16x16x4f32 with V widened and P in fp32.
-    static constexpr bool kHalfPV = LLKV_DECODE_HALF_PV && Elem<T>::kDtype != LLKV_DTYPE_F32 && D == 256;
+    static constexpr bool kHalfPV = Elem<T>::kDtype != LLKV_DTYPE_F32 && D == 256;
     // Resident waves per SIMD the register budget is held to: 5 (<= 96
     // registers) for head_dim 64; head_dim 128 needs more and gets 4.
     // head_dim 256: ~200 VGPRs (two waves per SIMD, no spills; three spill 33-49).
@@ -181,7 +175,7 @@ struct MfmaDecode {
     // its new-row pointers took it past the register budget (2-9 registers
     // spilled at head_dim 64, ~50 at 128); configuration 2 fused 25.9 ->
     // 24.5 us at four waves.
-    static constexpr bool kA32 = LLKV_DECODE_A4 && A && Elem<T>::kDtype == LLKV_DTYPE_F32;
+    static constexpr bool kA32 = A && Elem<T>::kDtype == LLKV_DTYPE_F32;
     static constexpr int kWavesPerEU =
         W > kDecodeWaves ? 4
                          : (D == 64 ? (kA32 ? 4 : 5) : (D == 96 ? 3 : (D == 128 ? (kA32 ? 3 : 4) : 2)));

@@ -8,10 +8,6 @@
 #include "decode_kernels.h"
 #include "decode_mfma.h"
 
-#ifndef LLKV_DECODE_D256
-#define LLKV_DECODE_D256 1
-#endif
-
 namespace llkv {
 namespace {
 
@@ -155,10 +151,8 @@ template <typename T>
 Kernels tuned(int D, int G, bool append) {
     if (D == 64) return append ? tuned_g<T, 64, true>(G) : tuned_g<T, 64, false>(G);
     if (D == 128) return append ? tuned_g<T, 128, true>(G) : tuned_g<T, 128, false>(G);
-#if LLKV_DECODE_D256
     if (D == 256) return append ? tuned_g_few<T, 256, true>(G) : tuned_g_few<T, 256, false>(G);
     if (D == 96) return append ? tuned_g_few<T, 96, true>(G) : tuned_g_few<T, 96, false>(G);
-#endif
     return Kernels();
 }
 

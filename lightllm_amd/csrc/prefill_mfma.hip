@@ -163,14 +163,11 @@ __device__ inline int ranked_unit(const MfmaPrefillArgs& a, int rank, const int*
     return u;
 }
 
-// Wave priority around the MFMA clusters (s_setprio: issue arbitration among
-// the waves of one SIMD, not a queue or stream priority).  1: the S = K Q^T
-// cluster runs at raised priority, so a wave in its matrix phase issues ahead
-// of waves in their softmax (configuration 5, head_dim 128: 210 -> 201 us;
-// neutral at head_dim 64, where it stays off); 2: the PV cluster too (no gain).
-#ifndef LLKV_PF_SETPRIO
-#define LLKV_PF_SETPRIO 1
-#endif
+// Wave priority around the S = K Q^T cluster (s_setprio: issue arbitration
+// among the waves of one SIMD, not a queue or stream priority): a wave in its
+// matrix phase issues ahead of waves in their softmax.  Measured at head_dim
+// 128 (configuration 5: 210 -> 201 us); neutral at head_dim 64, where it is
+// off.  Raising the PV cluster as well gained nothing.
 #define LLKV_PF_PRIO(on, p)                                \
     do {                                                   \
         if (on) {                                          \
@@ -180,24 +177,8 @@ __device__ inline int ranked_unit(const MfmaPrefillArgs& a, int rank, const int*
         }                                                  \
     } while (0)
 
-#ifndef LLKV_PF_UNROLL2
-#define LLKV_PF_UNROLL2 1
-#endif
-#ifndef LLKV_PREFILL_INTERLEAVE
-#define LLKV_PREFILL_INTERLEAVE 1
-#endif
-#ifndef LLKV_PF_DMA
-#define LLKV_PF_DMA 1
-#endif
-
 constexpr int kPageWindow = 256;   // page ids staged in LDS at a time
 
-#ifndef LLKV_PREFILL_XCD
-#define LLKV_PREFILL_XCD 1
-#endif
-#ifndef LLKV_PREFILL_REV
-#define LLKV_PREFILL_REV 1
-#endif
 constexpr int kXcds = 8;   // XCDs of an MI355X; work-groups go to them round-robin
 
 
@@ -224,25 +205,16 @@ __device__ inline bool take_work(const MfmaPrefillArgs& a, int* order, Work& wk)
     // so that the CU holding the longest item of the first set gets the
     // shortest of the second.
     int bid = blockIdx.x;
-#if LLKV_PREFILL_REV
     if (a.resident >= 2 * a.n_cus && bid >= a.n_cus && bid < 2 * a.n_cus) {
         const int hi = min(2 * a.n_cus, (int)gridDim.x);
         bid = a.n_cus + (hi - 1 - bid);
     }
-#endif
-#if LLKV_PREFILL_XCD
     const int xcd = bid % kXcds, r = bid / kXcds;
     const int j = (r / G) * kXcds + xcd;
     if (j >= a.groups) return false;
     wk.kvh = j % a.Hkv;
     wk.hq = wk.kvh * G + r % G;
     const int y = j / a.Hkv;
-#else
-    wk.hq = bid % a.Hq;
-    wk.kvh = wk.hq / G;
-    const int y = bid / a.Hq;
-    if (y * a.Hkv >= a.groups) return false;
-#endif
     // Every work-group takes the same decision from the same lengths.  Unsplit,
     // the first N x qblocks chunk slots are the units themselves (chunk 0) and
     // the other work-groups have nothing to do.
@@ -353,7 +325,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
 void prefill_mfma_kernel(MfmaPrefillArgs a) {
     // Direct-to-LDS staging (head_dim 64 / 128): wave w loads page w of the
     // tile (rows 16w .. 16w + 15) of K and of V, RPB rows per 1 KB block.
-    constexpr bool kDma = LLKV_PF_DMA && (D == 64 || D == 128);
+    constexpr bool kDma = D == 64 || D == 128;
     using SM = Smem<D, kDma>;
     constexpr int KPAD = SM::KPAD;
     constexpr int CPR = D / 8;            // 16-byte chunks per row
@@ -575,7 +547,7 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
             else load_tile(t + 1, kr, vr);
         }
         __builtin_amdgcn_sched_barrier(0);   // next tile's loads issue before this tile's MFMAs
-        LLKV_PF_PRIO(LLKV_PF_SETPRIO >= 1 && D >= 128, 1);
+        LLKV_PF_PRIO(D >= 128, 1);
 
         // ---- S^T = K Q^T over the 64 keys: 4 key tiles x 2 query tiles ----
         f32x4 s[4][2];
@@ -595,7 +567,7 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
             }
         }
 
-        LLKV_PF_PRIO(LLKV_PF_SETPRIO >= 1 && D >= 128, 0);
+        LLKV_PF_PRIO(D >= 128, 0);
         // ---- mask, online softmax (per query column) ----------------------
         // Scores stay raw (unscaled) until the exponent: p = 2^(s c - m) with
         // c = scale * log2(e) > 0, so the row maximum commutes with the scaling.
@@ -663,13 +635,11 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 pop[ss][nt].w = Mfma<T>::pack2(pv[1][2], pv[1][3]);
             }
         };
-#if LLKV_PREFILL_INTERLEAVE
         // The first half's MFMAs, each followed by a share of the second half's
         // exponentials; sched_barrier keeps this order (the scheduler would
         // otherwise put all VALU work first).  V^T rows of the second half are
         // read as those of the first are consumed.
         softmax_half(0);
-        LLKV_PF_PRIO(LLKV_PF_SETPRIO >= 2 && D >= 128, 1);
         {
             constexpr int kMf = 2 * DT + 2;   // MFMAs per half
             uint4 va0[DT], va1[DT];
@@ -710,24 +680,7 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) osum[nt] = Mfma<T>::mma(ones, pop[1][nt], osum[nt]);
         }
-#else
-        auto pv_half = [&](int ss) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const uint4 va = v_operand(buf, dt, ss);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt) o[dt][nt] = Mfma<T>::mma(va, pop[ss][nt], o[dt][nt]);
-            }
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) osum[nt] = Mfma<T>::mma(ones, pop[ss][nt], osum[nt]);
-        };
-        softmax_half(0);
-        pv_half(0);
-        softmax_half(1);
-        pv_half(1);
-#endif
 
-        LLKV_PF_PRIO(LLKV_PF_SETPRIO >= 2 && D >= 128, 0);
         if constexpr (kDma) {
             if (t + 1 < t_end) __builtin_amdgcn_s_waitcnt(0x3F70);   // vmcnt(0): tile t+1 in LDS
         } else {
@@ -735,7 +688,6 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
         }
         __syncthreads();
     };
-#if LLKV_PF_UNROLL2
     {
         int t = t_begin;
         for (; t + 1 < t_end; t += 2) {
@@ -744,9 +696,6 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
         }
         if (t < t_end) tile_step(t, std::integral_constant<int, 0>());
     }
-#else
-    for (int t = t_begin; t < t_end; ++t) tile_step(t, (t - t_begin) & 1);
-#endif
 
     // ---- normalise and write: lane holds dims dt*16 + 4g + i of its query --
     // (one chunk: the output row; several: an fp32 partial row + log2-sum-exp2,
@@ -801,31 +750,10 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
 // The S = K Q^T cluster at raised wave priority (as in the 16-bit kernel):
 // configuration 4's shape in fp32 360-380 -> 339-344 us; neutral at
 // head_dim 128 (one wave per SIMD).
-#ifndef LLKV_F32_SETPRIO
-#define LLKV_F32_SETPRIO 1
-#endif
-#ifndef LLKV_F32_KNB64
-#define LLKV_F32_KNB64 2
-#endif
-#ifndef LLKV_F32_VNB64
-#define LLKV_F32_VNB64 1
-#endif
-#ifndef LLKV_F32_WPE64
-#define LLKV_F32_WPE64 3
-#endif
-#ifndef LLKV_F32_WPE128
-#define LLKV_F32_WPE128 1
-#endif
-#ifndef LLKV_F32_KNB128
-#define LLKV_F32_KNB128 2
-#endif
-#ifndef LLKV_F32_VNB128
-#define LLKV_F32_VNB128 2
-#endif
 template <int D>
 struct SmemF32 {
-    static constexpr int KNB = D == 64 ? LLKV_F32_KNB64 : (D == 128 ? LLKV_F32_KNB128 : 1);
-    static constexpr int VNB = D == 64 ? LLKV_F32_VNB64 : (D == 128 ? LLKV_F32_VNB128 : 1);   // 96, 256: 1
+    static constexpr int KNB = D == 64 || D == 128 ? 2 : 1;
+    static constexpr int VNB = D == 128 ? 2 : 1;   // 64, 96, 256: 1
     static constexpr int KPAD = D + 4;    // floats per K row (pad: 16-byte reads of 16 rows hit distinct banks)
     static constexpr int VPAD = BN + 4;   // floats per V^T row
     union {
@@ -839,7 +767,7 @@ struct SmemF32 {
 };
 
 template <int D, bool CG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? LLKV_F32_WPE64 : (D == 96 ? 2 : LLKV_F32_WPE128))))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 3 : (D == 96 ? 2 : 1))))
 void prefill_f32_kernel(MfmaPrefillArgs a) {
     typedef SmemF32<D> S;
     constexpr int KPAD = S::KPAD, VPAD = S::VPAD, KNB = S::KNB, VNB = S::VNB;
@@ -1004,7 +932,7 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
 
-        LLKV_PF_PRIO(LLKV_F32_SETPRIO, 1);
+        LLKV_PF_PRIO(true, 1);
         // ---- S^T = K Q^T: key tile kt holds keys 16kt .. 16kt+15 ---------
         // The two halves of the head dims accumulate apart and are added at
         // the end: half the rounding steps in each sum, which halves the
@@ -1034,7 +962,7 @@ void prefill_f32_kernel(MfmaPrefillArgs a) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) s[kt][nt] += hi[nt];
         }
-        LLKV_PF_PRIO(LLKV_F32_SETPRIO, 0);
+        LLKV_PF_PRIO(true, 0);
         if (next) {
             if (KNB == 1) __syncthreads();   // every wave is done with the K buffer
             store_k(KNB == 2 ? kbuf ^ 1 : 0);
@@ -1243,10 +1171,7 @@ bool prefill_mfma_handles(int head_dim, int block_size, int dtype) {
 // work-group per slot: with fp32 partials, configuration 4 runs two chunks
 // per long unit at 58.1 us against 59.8 us for three (1.5 per slot) and
 // 80 us for two per slot; the fewer chunks, the less partial traffic.
-#ifndef LLKV_PREFILL_FILL
-#define LLKV_PREFILL_FILL 1.0
-#endif
-constexpr double kFill = LLKV_PREFILL_FILL;
+constexpr double kFill = 1.0;
 constexpr int kMinChunkTiles = 8;
 constexpr int kSizingSlots = 1024;
 

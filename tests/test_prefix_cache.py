@@ -9,6 +9,11 @@
   (tests/test_prefix_cache.cpp, tests/test_radix_engine.cpp) are compiled against
   this build's headers and sources (oracle/_ref/*_ours) and must pass, and
   fresh seeds are diffed live against the reference build.
+* Sanitizers: this build's host C++ (allocator, caches, C handle API, host Tensor)
+  runs under AddressSanitizer + UndefinedBehaviorSanitizer, with leak checks: the
+  trace driver (oracle/_bin/trace_ours_san), the reference's test programs built on
+  this build's sources (oracle/_ref/*_ours_san), and a seeded serving-workload
+  driver (tests/cpp/test_host_san.cpp).
 * The allocator handle (C ABI, metadata-only storage) follows the reference's
   allocator checks (tests/test_paged_attention_v2.cu:610-637) and the FIFO /
   hash-probe / eviction rules of src/kv_cache/block_allocator.cpp:33-147.
@@ -22,11 +27,13 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = os.path.join(ROOT, "tests", "golden", "prefix_cache")
 TRACE_OURS = os.path.join(ROOT, "oracle", "_bin", "trace_ours")
+TRACE_SAN = os.path.join(ROOT, "oracle", "_bin", "trace_ours_san")
+HOST_SAN = os.path.join(ROOT, "tests", "cpp", "_bin", "test_host_san")
 REF_DIR = os.path.join(ROOT, "oracle", "_ref")
 
 
-def _trace(exe, policy, bs, seed, n_ops, pool):
-    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0")
+def _trace(exe, policy, bs, seed, n_ops, pool, leaks=False):
+    env = dict(os.environ, ASAN_OPTIONS=f"detect_leaks={int(leaks)}")
     r = subprocess.run([exe, policy, str(bs), str(seed), str(n_ops), str(pool)],
                        capture_output=True, text=True, env=env, timeout=120)
     return r.returncode, [l for l in r.stdout.splitlines() if l]
@@ -57,6 +64,39 @@ def test_trace_matches_reference_golden(path):
     assert len(ours) == ops + 1
     for i, (g, o) in enumerate(zip(golden, ours)):
         assert g == o, f"line {i}: reference {g!r} vs ours {o!r}"
+
+
+@pytest.mark.parametrize("path", GOLDEN_FILES[:4], ids=[os.path.basename(p) for p in GOLDEN_FILES[:4]])
+def test_trace_under_sanitizers(path):
+    """The same golden traces from this build's caches built with ASan + UBSan (and leak
+    checks): no memory error, no undefined behaviour, the same lines."""
+    assert os.path.exists(TRACE_SAN), "run make -C oracle all"
+    policy, bs, seed, ops, pool = _parse(path)
+    with open(path) as f:
+        golden = [l for l in f.read().splitlines() if l]
+    rc, ours = _trace(TRACE_SAN, policy, bs, seed, ops, pool, leaks=True)
+    assert rc == 0
+    assert ours[:len(golden)] == golden[:len(ours)] and len(ours) == ops + 1
+
+
+def _build_host_san():
+    if not os.path.exists(HOST_SAN):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "tests", "cpp"), "san"], check=True,
+                       capture_output=True, timeout=600)
+
+
+@pytest.mark.parametrize("seed", [1, 7, 42])
+def test_host_code_under_sanitizers(seed):
+    """Seeded serving workload over BlockAllocator (host and metadata-only pools, both
+    policies), the C handle API and the host Tensor, built with ASan + UBSan
+    (tests/cpp/test_host_san.cpp): every check passes and the sanitizers report nothing
+    (they abort on the first finding, leaks included)."""
+    _build_host_san()
+    r = subprocess.run([HOST_SAN, str(seed)], capture_output=True, text=True, timeout=300,
+                       env=dict(os.environ, ASAN_OPTIONS="detect_leaks=1",
+                                UBSAN_OPTIONS="print_stacktrace=1"))
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert " 0 failed" in r.stdout, r.stdout[-2000:]
 
 
 def test_traces_exercise_every_op_kind():
@@ -93,9 +133,13 @@ def test_trace_live_vs_reference(policy, seed):
 
 @pytest.mark.skipif(not os.path.exists(os.path.join(REF_DIR, "test_prefix_cache_ours")),
                     reason="reference tests not built here (oracle/_ref)")
-@pytest.mark.parametrize("prog", ["test_prefix_cache_ours", "test_radix_engine_ours"])
+@pytest.mark.parametrize("prog", ["test_prefix_cache_ours", "test_radix_engine_ours",
+                                  "test_prefix_cache_ours_san", "test_radix_engine_ours_san"])
 def test_reference_cache_tests_pass_on_this_build(prog):
-    r = subprocess.run([os.path.join(REF_DIR, prog)], capture_output=True, text=True, timeout=300)
+    """The reference's own cache test programs on this build's sources (the _san builds under
+    ASan + UBSan with leak checks)."""
+    r = subprocess.run([os.path.join(REF_DIR, prog)], capture_output=True, text=True, timeout=300,
+                       env=dict(os.environ, ASAN_OPTIONS="detect_leaks=1"))
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     assert "FAIL" not in r.stdout.replace("0 failed", "")
 
