@@ -34,7 +34,15 @@ Profiling helpers (the commands that produce the summaries under profiles/):
                                             GRBM_GUI_ACTIVE counter run
   python bench.py --profile-target NAME     eager calls of one workload (cfg2_decode,
                                             cfg3_decode, cfg5_decode, cfg4_prefill,
-                                            cfg5_prefill) for rocprofv3
+                                            cfg5_prefill, ceiling_cfg2/3/5) for rocprofv3
+  python bench.py --read-ceiling CFG        read ceiling of decode configuration CFG
+                                            (cfg2, cfg3, cfg5) beside its decode
+
+Read ceiling: measurement-only kernels (lightllm_amd/csrc/read_ceiling.hip, their
+own library) read exactly a decode batch's K/V rows -- the same page ids, the
+same (page, kv head) pieces, the same rotated pools, HIP-graph replays -- and
+nothing else.  Their time bounds any decode of that batch on this GPU;
+roofline.frac_of_ceiling = ceiling time / decode time.
 """
 from __future__ import annotations
 
@@ -158,6 +166,9 @@ def bench_decode(args, torch, kc, wl):
     step_us = replay_us(step, args.steps)
     dec_us = replay_us(decode_only, args.steps)
     fused_us = replay_us(step_fused, args.steps)
+    sched = kc.decode_schedule(B, hq, hkv, d, max_len, torch.float32)
+    ceiling, _ = read_ceiling(torch, list(zip(kps, vps)), table, lens, hkv, d, 4,
+                              sched[1] if sched[0] in ("splits", "unit") else 0, args.steps)
 
     # Eager loop with HIP events around each decode call (host-launch gaps included).
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -188,7 +199,7 @@ def bench_decode(args, torch, kc, wl):
         "decode_bytes": dec_bytes, "decode_bytes_pages": dec_bytes_pages, "append_bytes": app_bytes,
         "pool_bytes": 2 * kps[0].numel() * kps[0].element_size(),
         "parity_ok": ok, "max_abs_err": float(err.max()),
-        "schedule": kc.decode_schedule(B, hq, hkv, d, max_len, torch.float32),
+        "schedule": sched, "ceiling": ceiling,
     }
 
 
@@ -237,6 +248,146 @@ def _graph_us(torch, fn, n, warm_replays=3, timed_replays=5):
     return statistics.median(times)
 
 
+CEIL_LIB = os.path.join(ROOT, "lightllm_amd", "liblightllm_kv_ceiling.so")
+_ceil = None
+
+
+def _ceiling_lib():
+    """The measurement-only read-ceiling kernels (lightllm_amd/csrc/read_ceiling.hip)."""
+    global _ceil
+    if _ceil is None:
+        import ctypes
+        from ctypes import c_int, c_int64, c_void_p
+        if not os.path.exists(CEIL_LIB):
+            raise SystemExit(f"{CEIL_LIB} is missing: run __graft_entry__.build()")
+        lib = ctypes.CDLL(CEIL_LIB)
+        lib.llkv_rc_flat.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64, c_int, c_void_p,
+                                     c_void_p]
+        lib.llkv_rc_chain.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
+                                      c_int, c_void_p, c_void_p]
+        lib.llkv_rc_flat_resident.argtypes = [c_int]
+        _ceil = lib
+    return _ceil
+
+
+def ceiling_items(torch, table, lens, hkv, piece_bytes, dev):
+    """The batch's (page, kv head) pieces in the pool, in decode order (sequence, page, kv
+    head): int64 (byte offset of the piece's row 0) << 5 | rows holding tokens."""
+    import numpy as np
+    t = table.cpu().numpy().astype(np.int64)
+    L = lens.cpu().numpy().astype(np.int64)
+    row = piece_bytes * hkv
+    items = []
+    for b in range(t.shape[0]):
+        n = int((L[b] + 15) // 16)
+        if n == 0:
+            continue
+        p = np.arange(n)
+        rows = np.minimum(16, L[b] - 16 * p)
+        base = t[b, :n] * 16 * row
+        it = ((base[:, None] + np.arange(hkv)[None, :] * piece_bytes) << 5) | rows[:, None]
+        items.append(it.reshape(-1))
+    return torch.from_numpy(np.concatenate(items)).to(dev)
+
+
+def read_ceiling(torch, pools, table, lens, hkv, d, esize, splits, calls, timed=True):
+    """Per-call time of the read-ceiling kernels over a batch's exact pages, HIP-graph replays of
+    `calls` calls rotating over `pools` [(k, v)], as the decode benches run: 'flat' (pure read
+    of the (page, kv head) pieces, one resident set of work-groups) and, for splits > 0,
+    'chain' (the fixed-split decode's length -> table -> page walk, no arithmetic)."""
+    lib = _ceiling_lib()
+    dev = pools[0][0].device
+    piece = d * esize
+    items = ceiling_items(torch, table, lens, hkv, piece, dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    nwg = lib.llkv_rc_flat_resident(piece)
+    if nwg <= 0:
+        raise RuntimeError("read ceiling: no resident work-groups")
+    tb, ln = table.to(dev), lens.to(dev)
+    res = {"pieces": int(items.numel()), "workgroups": nwg}
+
+    def flat(i):
+        k, v = pools[i % len(pools)]
+        st = torch.cuda.current_stream().cuda_stream
+        rc = lib.llkv_rc_flat(k.data_ptr(), v.data_ptr(), items.data_ptr(), int(items.numel()), piece,
+                              piece * hkv, nwg, sink.data_ptr(), st)
+        assert rc == 0, rc
+
+    def chain(i):
+        k, v = pools[i % len(pools)]
+        st = torch.cuda.current_stream().cuda_stream
+        rc = lib.llkv_rc_chain(k.data_ptr(), v.data_ptr(), tb.data_ptr(), ln.data_ptr(), tb.shape[1],
+                               tb.shape[0], hkv, splits, piece, sink.data_ptr(), st)
+        assert rc == 0, rc
+
+    if not timed:   # the calls only (rocprofv3 runs)
+        return res, (flat, chain)
+    for i in range(2 * len(pools)):
+        flat(i)
+    torch.cuda.synchronize()
+    res["flat_us"] = _graph_us(torch, flat, calls)
+    if splits > 0:
+        res["chain_us"] = _graph_us(torch, chain, calls)
+        res["chain_splits"] = splits
+    return res, (flat, chain)
+
+
+def ceiling_setup(torch, kc, wl, name):
+    """Pools, tables and the decode call of one decode configuration, as the main bench builds
+    them (configuration 2: 8 layer pools; 3: 2; 5: its one 262144-page pool)."""
+    dev = torch.device("cuda:0")
+    if name == "cfg5":
+        case = wl.config5().decode
+        pools = [wl.device_pools(262144, 8, 128, torch.float16, 55, dev)]
+    else:
+        case = wl.config2() if name == "cfg2" else wl.config3()
+        nb, hkv, d = case.k_pool.shape[0], case.k_pool.shape[2], case.k_pool.shape[3]
+        layers = 8 if name == "cfg2" else 2
+        pools = [wl.device_pools(nb, hkv, d, case.k_pool.dtype, 100 + i, dev) for i in range(layers)]
+    B, hq, d = case.q.shape
+    hkv = pools[0][0].shape[2]
+    q, bt, sl = case.q.to(dev), case.block_table.to(dev), case.seq_lens.to(dev)
+    out = torch.empty_like(q)
+    ml = case.max_seq_len
+    ws = kc._workspace(kc.decode_workspace_bytes(B, hq, hkv, d, 16, ml), dev)
+    dec = lambda i: kc.paged_decode(q, pools[i % len(pools)][0], pools[i % len(pools)][1], bt, sl, ml,
+                                    out=out, workspace=ws)
+    sched = kc.decode_schedule(B, hq, hkv, d, ml, case.q.dtype)
+    return {"case": case, "pools": pools, "table": bt, "lens": sl, "hkv": hkv, "d": d,
+            "esize": case.q.element_size(), "decode": dec, "bytes": wl.decode_bytes(case),
+            "schedule": sched, "splits": sched[1] if sched[0] in ("splits", "unit") else 0}
+
+
+def ceiling_fields(rc, decode_us, nbytes):
+    """Bench-line fields of a read-ceiling result: the ceiling as a rate over the decode's own
+    algorithmic bytes, and the decode's fraction of it (ceiling time / decode time)."""
+    out = {"ceiling_us": round(rc["flat_us"], 2),
+           "ceiling_GBps": round(nbytes / (rc["flat_us"] * 1e-6) / 1e9, 1),
+           "frac_of_ceiling": round(rc["flat_us"] / decode_us, 4)}
+    if "chain_us" in rc:
+        out["chain_ceiling_us"] = round(rc["chain_us"], 2)
+        out["chain_splits"] = rc["chain_splits"]
+    return out
+
+
+def read_ceiling_mode(torch, kc, wl, name, calls):
+    """--read-ceiling NAME: the read ceiling of one decode configuration and its decode, HIP-graph
+    replays of `calls` calls over the same rotated pools; one JSON line."""
+    st = ceiling_setup(torch, kc, wl, name)
+    for i in range(3):
+        st["decode"](i)
+    torch.cuda.synchronize()
+    dec_us = _graph_us(torch, st["decode"], calls)
+    rc, _ = read_ceiling(torch, st["pools"], st["table"], st["lens"], st["hkv"], st["d"], st["esize"],
+                         st["splits"], calls)
+    line = {"read_ceiling": name, "decode_us": round(dec_us, 2),
+            "decode_GBps": round(st["bytes"] / (dec_us * 1e-6) / 1e9, 1),
+            "decode_schedule": list(st["schedule"]), "bytes_per_call": st["bytes"],
+            "pieces": rc["pieces"], "workgroups": rc["workgroups"], "pools_rotated": len(st["pools"])}
+    line.update(ceiling_fields(rc, dec_us, st["bytes"]))
+    print(json.dumps(line), flush=True)
+
+
 def bench_other_configs(torch, kc, wl):
     """Configurations 3 and 5 (decode HBM rate, prefill MFMA rate), HIP-graph replays."""
     dev = torch.device("cuda:0")
@@ -258,6 +409,12 @@ def bench_other_configs(torch, kc, wl):
                                     "GBps": round(wl.decode_bytes(c3) / (us * 1e-6) / 1e9, 1),
                                     "GBps_page_granular": round(wl.decode_bytes(c3, exact_tokens=False)
                                                                 / (us * 1e-6) / 1e9, 1)}
+        if S == 0:
+            s3 = kc.decode_schedule(c3.q.shape[0], c3.q.shape[1], 2, 64, c3.max_seq_len, torch.float16)
+            rc3, _ = read_ceiling(torch, pools, bt, sl, 2, 64, 2,
+                                  s3[1] if s3[0] in ("splits", "unit") else 0, 20)
+            res["cfg3_decode_S0"]["schedule"] = list(s3)
+            res["cfg3_decode_S0"].update(ceiling_fields(rc3, us, wl.decode_bytes(c3)))
     del pools
     m5 = wl.config5()
     dec, pre = m5.decode, m5.prefill
@@ -279,10 +436,12 @@ def bench_other_configs(torch, kc, wl):
     pre_us = _graph_us(torch, lambda i: kc.paged_prefill(pq, kp, vp, pbt, pcu, psl, pre.max_q_len,
                                                          pre.max_seq_len, True, out=pout), 5)
     pf = wl.prefill_flops(pre)
+    rc5, _ = read_ceiling(torch, [(kp, vp)], dbt, dsl, 8, 128, 2, 0, 5)
     res["cfg5_step"] = {"us": round(step_us, 1), "decode_us": round(dec_us, 1),
                         "decode_GBps": round(wl.decode_bytes(dec) / (dec_us * 1e-6) / 1e9, 1),
                         "decode_GBps_page_granular": round(wl.decode_bytes(dec, exact_tokens=False)
                                                            / (dec_us * 1e-6) / 1e9, 1),
+                        "decode_ceiling": ceiling_fields(rc5, dec_us, wl.decode_bytes(dec)),
                         "prefill_us": round(pre_us, 1),
                         "prefill_mfma_frac": round(pf / (pre_us * 1e-6) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4)}
     res["rope_append_cfg5_step"] = bench_rope_append(torch, kc, dec, pre, kp, vp, dsl_slots, pslots)
@@ -624,6 +783,13 @@ def profile_target(torch, kc, wl, name: str, iters: int) -> None:
             fn = lambda i: kc.paged_prefill(q, kp, vp, bt, cu, sl, c.max_q_len, c.max_seq_len, True,
                                             out=out)
             what = f"{name}: llkv_paged_prefill, {wl.prefill_flops(c)} FLOP per call"
+    elif name.startswith("ceiling_"):
+        st = ceiling_setup(torch, kc, wl, name[len("ceiling_"):])
+        _, (flat, chain) = read_ceiling(torch, st["pools"], st["table"], st["lens"], st["hkv"], st["d"],
+                                        st["esize"], st["splits"], 2, timed=False)
+        fn = flat
+        what = (f"{name}: llkv_rc_flat over the decode's pages, {len(st['pools'])} pools rotated, "
+                f"{st['bytes']} B of decode per call")
     elif name == "cfg4_prefill":
         c = wl.config4()
         kp, vp = c.k_pool.to(dev), c.v_pool.to(dev)
@@ -643,7 +809,8 @@ def profile_target(torch, kc, wl, name: str, iters: int) -> None:
     print(json.dumps({"profile_target": what, "calls": iters}), flush=True)
 
 
-PROFILE_TARGETS = ("cfg2_decode", "cfg3_decode", "cfg5_decode", "cfg4_prefill", "cfg5_prefill")
+PROFILE_TARGETS = ("cfg2_decode", "cfg3_decode", "cfg5_decode", "cfg4_prefill", "cfg5_prefill",
+                   "ceiling_cfg2", "ceiling_cfg3", "ceiling_cfg5")
 
 
 def main():
@@ -663,6 +830,8 @@ def main():
     ap.add_argument("--profile-target", choices=PROFILE_TARGETS,
                     help="eager launches of one workload for rocprofv3, no JSON line")
     ap.add_argument("--profile-iters", type=int, default=20)
+    ap.add_argument("--read-ceiling", choices=("cfg2", "cfg3", "cfg5"),
+                    help="read ceiling of one decode configuration beside its decode, one JSON line")
     args = ap.parse_args()
     if args.rocprof_summary:
         rocprof_summary(args.rocprof_summary)
@@ -686,6 +855,9 @@ def main():
     from lightllm_amd import workloads as wl
     if args.profile_target:
         profile_target(torch, kc, wl, args.profile_target, args.profile_iters)
+        return
+    if args.read_ceiling:
+        read_ceiling_mode(torch, kc, wl, args.read_ceiling, max(20, args.steps // 4))
         return
 
     dec = bench_decode(args, torch, kc, wl)
@@ -729,6 +901,11 @@ def main():
                                    "decode_split_kernel<MfmaDecode<float,64,7>> then decode_merge_kernel<float,1>"
                                    if dec["schedule"][0] == "splits" else "the kernels of that schedule"),
                      "bytes_per_launch": dec["decode_bytes"],
+                     **ceiling_fields(dec["ceiling"], dec["decode_us_mean"], dec["decode_bytes"]),
+                     "ceiling_note": "read ceiling: lightllm_amd/csrc/read_ceiling.hip reads exactly this "
+                                     "batch's K/V rows (same pages, pieces, rotated pools, graph replay) "
+                                     "and nothing else; ceiling_GBps counts the decode's algorithmic bytes "
+                                     "over that time, frac_of_ceiling = ceiling time / decode time",
                      "timing": "HIP events on the launch stream around a HIP-graph replay of "
                                f"--steps llkv_paged_decode calls ({args.layers} layer pools rotated, "
                                "so a rotation touches more than twice the 256 MB last-level cache)"},
