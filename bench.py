@@ -168,7 +168,7 @@ def bench_decode(args, torch, kc, wl):
     fused_us = replay_us(step_fused, args.steps)
     sched = kc.decode_schedule(B, hq, hkv, d, max_len, torch.float32)
     ceiling, _ = read_ceiling(torch, list(zip(kps, vps)), table, lens, hkv, d, 4,
-                              sched[1] if sched[0] in ("splits", "unit") else 0, args.steps)
+                              sched[1] if sched[0] == "splits" else 0, args.steps)
 
     # Eager loop with HIP events around each decode call (host-launch gaps included).
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -294,7 +294,8 @@ def read_ceiling(torch, pools, table, lens, hkv, d, esize, splits, calls, timed=
     """Per-call time of the read-ceiling kernels over a batch's exact pages, HIP-graph replays of
     `calls` calls rotating over `pools` [(k, v)], as the decode benches run: 'flat' (pure read
     of the (page, kv head) pieces, one resident set of work-groups) and, for splits > 0,
-    'chain' (the fixed-split decode's length -> table -> page walk, no arithmetic)."""
+    'chain' (the fixed-split decode's length -> table -> page walk on 4-wave work-groups, no
+    arithmetic; reported for the fixed-split schedule only)."""
     lib = _ceiling_lib()
     dev = pools[0][0].device
     piece = d * esize
@@ -355,7 +356,7 @@ def ceiling_setup(torch, kc, wl, name):
     sched = kc.decode_schedule(B, hq, hkv, d, ml, case.q.dtype)
     return {"case": case, "pools": pools, "table": bt, "lens": sl, "hkv": hkv, "d": d,
             "esize": case.q.element_size(), "decode": dec, "bytes": wl.decode_bytes(case),
-            "schedule": sched, "splits": sched[1] if sched[0] in ("splits", "unit") else 0}
+            "schedule": sched, "splits": sched[1] if sched[0] == "splits" else 0}
 
 
 def ceiling_fields(rc, decode_us, nbytes):
@@ -412,7 +413,7 @@ def bench_other_configs(torch, kc, wl):
         if S == 0:
             s3 = kc.decode_schedule(c3.q.shape[0], c3.q.shape[1], 2, 64, c3.max_seq_len, torch.float16)
             rc3, _ = read_ceiling(torch, pools, bt, sl, 2, 64, 2,
-                                  s3[1] if s3[0] in ("splits", "unit") else 0, 20)
+                                  s3[1] if s3[0] == "splits" else 0, 20)
             res["cfg3_decode_S0"]["schedule"] = list(s3)
             res["cfg3_decode_S0"].update(ceiling_fields(rc3, us, wl.decode_bytes(c3)))
     del pools
