@@ -152,9 +152,10 @@ int llkv_rope_append(void* q, void* k, const void* v, void* k_pool, void* v_pool
  *              without the reference's device-to-host read).
  * num_splits : 0 = automatic, chosen from the kernel's resident work-group
  *              count: with few (sequence, kv head) units each is cut into
- *              S ~ resident / units fixed splits (0.8 x that when the longest
- *              sequence gives a wave more than 4 pages; at most one split per
- *              4 pages); with many (up to 1024
+ *              S ~ resident / units fixed splits (when the longest sequence
+ *              gives a wave more than 4 pages: 16-wave work-groups, one per
+ *              CU, or 0.8 x the 4-wave count; at most one split per 4
+ *              pages); with many (up to 1024
  *              sequences) the batch's pages are shared equally among one
  *              resident set of work-groups, whatever the length mix (larger
  *              batches use 8-page splits);

@@ -390,11 +390,15 @@ AutoChoice auto_schedule(const Kernels& ks, int B, int Hkv, int max_pages) {
     // the chains are long (bandwidth-bound: extra work-groups only contend).
     int64_t S = (cap + units - 1) / units;
     if ((int64_t)max_pages > S * kDecodeWaves * kShortChainPages) {
-        // Long chains: the 16-wave kernel at 0.8 of its resident count, a
-        // quarter as many splits (and partials to merge) for the same waves.
+        // Long chains: the 16-wave kernel at its full resident count (one
+        // work-group per CU), a quarter as many splits (and partials to merge)
+        // for the same waves.  Full rather than 0.8 x (which left a fifth of
+        // the CUs idle): configuration 3 55.6 -> 55.2 us, 8 x 32k tokens 29.9 ->
+        // 29.0 us, 32/8/128 fp16 4 x 32k 112.6 -> 110.1 us, equal on the other
+        // long-chain shapes swept; twice the resident count was slower.
         if (ks.unit != nullptr) {
             const int cap16 = resident_workgroups(reinterpret_cast<const void*>(ks.unit), 64 * kUnitWaves);
-            const int64_t S16 = std::min<int64_t>((cap16 * 4 / 5 + units - 1) / units, kAutoMaxSplits);
+            const int64_t S16 = std::min<int64_t>((cap16 + units - 1) / units, kAutoMaxSplits);
             if (S16 > 1 && (int64_t)max_pages > S16 * kUnitWaves * kShortChainPages) {
                 c.wide = true;
                 c.splits = (int)S16;

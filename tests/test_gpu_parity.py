@@ -595,7 +595,7 @@ def test_decode_schedule_query():
     assert q(1, 14, 2, 64, 513, torch.float32) == ("splits", 9)          # configuration 1
     assert q(64, 14, 2, 64, 2049, torch.float32) == ("splits", 10)       # configuration 2
     # configuration 3: few units with long chains take 16-wave work-groups in fixed splits
-    assert q(16, 14, 2, 64, 32768, torch.float16) == ("unit", 7)
+    assert q(16, 14, 2, 64, 32768, torch.float16) == ("unit", 8)
     assert q(256, 32, 8, 128, 16385, torch.float16)[0] == "balanced"     # configuration 5 decode
     assert q(512, 14, 2, 64, 101, torch.bfloat16) == ("one_split", 1)    # <= 8 pages
     assert q(24, 32, 8, 128, 701, torch.float16) == ("unit", 1)          # 16-wave work-groups
