@@ -265,9 +265,9 @@ def _ceiling_lib():
             raise SystemExit(f"{CEIL_LIB} is missing: run __graft_entry__.build()")
         lib = ctypes.CDLL(CEIL_LIB)
         lib.llkv_rc_flat.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64, c_int, c_void_p,
-                                     c_void_p]
+                                     c_int, c_void_p]
         lib.llkv_rc_chain.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
-                                      c_int, c_void_p, c_void_p]
+                                      c_int, c_void_p, c_int, c_void_p]
         lib.llkv_rc_flat_resident.argtypes = [c_int]
         _ceil = lib
     return _ceil
@@ -303,25 +303,26 @@ def read_ceiling(torch, pools, table, lens, hkv, d, esize, splits, calls, timed=
     dev = pools[0][0].device
     piece = d * esize
     items = ceiling_items(torch, table, lens, hkv, piece, dev)
-    sink = torch.zeros(4, dtype=torch.int32, device=dev)
     nwg = lib.llkv_rc_flat_resident(piece)
     if nwg <= 0:
         raise RuntimeError("read ceiling: no resident work-groups")
     tb, ln = table.to(dev), lens.to(dev)
+    # one checksum word per wave (4 per work-group) of either kernel
+    sink = torch.zeros(4 * max(nwg, max(splits, 1) * hkv * tb.shape[0]), dtype=torch.int32, device=dev)
     res = {"pieces": int(items.numel()), "workgroups": nwg}
 
     def flat(i):
         k, v = pools[i % len(pools)]
         st = torch.cuda.current_stream().cuda_stream
         rc = lib.llkv_rc_flat(k.data_ptr(), v.data_ptr(), items.data_ptr(), int(items.numel()), piece,
-                              piece * hkv, nwg, sink.data_ptr(), st)
+                              piece * hkv, nwg, sink.data_ptr(), 0, st)
         assert rc == 0, rc
 
     def chain(i):
         k, v = pools[i % len(pools)]
         st = torch.cuda.current_stream().cuda_stream
         rc = lib.llkv_rc_chain(k.data_ptr(), v.data_ptr(), tb.data_ptr(), ln.data_ptr(), tb.shape[1],
-                               tb.shape[0], hkv, splits, piece, sink.data_ptr(), st)
+                               tb.shape[0], hkv, splits, piece, sink.data_ptr(), 0, st)
         assert rc == 0, rc
 
     if not timed:   # the calls only (rocprofv3 runs)
