@@ -436,12 +436,14 @@ def bench_other_configs(torch, kc, wl):
         kc.paged_decode(dq, kp, vp, dbt, dsl, dec.max_seq_len, out=dout)
         kc.paged_prefill(pq, kp, vp, pbt, pcu, psl, pre.max_q_len, pre.max_seq_len, True, out=pout)
 
-    step_us = _graph_us(torch, step, 5)
-    dec_us = _graph_us(torch, lambda i: kc.paged_decode(dq, kp, vp, dbt, dsl, dec.max_seq_len, out=dout), 5)
+    # 20 calls per graph, so that the replay's start-up cost is spread thin
+    n5 = 20
+    step_us = _graph_us(torch, step, n5)
+    dec_us = _graph_us(torch, lambda i: kc.paged_decode(dq, kp, vp, dbt, dsl, dec.max_seq_len, out=dout), n5)
     pre_us = _graph_us(torch, lambda i: kc.paged_prefill(pq, kp, vp, pbt, pcu, psl, pre.max_q_len,
-                                                         pre.max_seq_len, True, out=pout), 5)
+                                                         pre.max_seq_len, True, out=pout), n5)
     pf = wl.prefill_flops(pre)
-    rc5, _ = read_ceiling(torch, [(kp, vp)], dbt, dsl, 8, 128, 2, 0, 5)
+    rc5, _ = read_ceiling(torch, [(kp, vp)], dbt, dsl, 8, 128, 2, 0, n5)
     res["cfg5_step"] = {"us": round(step_us, 1), "decode_us": round(dec_us, 1),
                         "decode_GBps": round(wl.decode_bytes(dec) / (dec_us * 1e-6) / 1e9, 1),
                         "decode_GBps_page_granular": round(wl.decode_bytes(dec, exact_tokens=False)

@@ -275,9 +275,13 @@ __device__ inline void poison_uncovered_rows(const MfmaPrefillArgs& a, const Wor
 // it before every LDS read of the other buffer; the caller waits (vmcnt) before
 // the barrier that publishes the tile.  A later load only lengthens the
 // compiler's own in-order vmcnt waits.
-__device__ inline void dma16(const void* gptr, const void* lds) {
-    const uint32_t la = __builtin_amdgcn_readfirstlane(
+// la: the LDS byte address (lds_addr), wave-uniform.
+__device__ inline uint32_t lds_addr(const void* lds) {
+    return __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+}
+
+__device__ inline void dma16(const void* gptr, uint32_t la) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :
                  : "v"(gptr), "s"(la)
@@ -286,9 +290,7 @@ __device__ inline void dma16(const void* gptr, const void* lds) {
 
 // The same with a wave-uniform base (scalar registers) and a 32-bit per-lane
 // byte offset (no per-lane 64-bit address arithmetic).
-__device__ inline void dma16_s(const void* sbase, uint32_t voff, const void* lds) {
-    const uint32_t la = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+__device__ inline void dma16_s(const void* sbase, uint32_t voff, uint32_t la) {
     const uint64_t b = (uint64_t)(uintptr_t)sbase;
     // (readfirstlane returns int: widen through uint32_t, not by sign extension)
     const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)) << 32) |
@@ -497,6 +499,17 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
         dma_row[j] = r;
         dma_off[j] = (CG ? 0u : (uint32_t)r * row_bytes) + (uint32_t)c * 16u;
     }
+    // LDS byte addresses of the wave's blocks in each buffer, computed once
+    // (scalar registers; the loop then only moves them to M0).
+    uint32_t lds_k[2][BPW], lds_v[2][BPW];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < BPW; ++j) {
+            const int lrow = 16 * w + j * RPB;
+            lds_k[b][j] = lds_addr(&sm.k[b][lrow * KPAD]);
+            lds_v[b][j] = lds_addr(&sm.v[b][lrow * KPAD]);
+        }
     auto dma_tile = [&](int t, int buf) {
         if constexpr (kDma) {
             if constexpr (CG) {
@@ -504,9 +517,8 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 for (int j = 0; j < BPW; ++j) {   // rows past the sequence's last are staged as the last
                     const int key = min(t * BN + 16 * w + dma_row[j], L - 1);
                     const uint64_t off = (uint64_t)key * row_bytes + dma_off[j];
-                    const int lrow = 16 * w + j * RPB;
-                    dma16(kb + off, &sm.k[buf][lrow * KPAD]);
-                    dma16(vb + off, &sm.v[buf][lrow * KPAD]);
+                    dma16(kb + off, lds_k[buf][j]);
+                    dma16(vb + off, lds_v[buf][j]);
                 }
             } else {
                 // the wave's page: one scalar base per pool, 32-bit lane offsets
@@ -514,9 +526,8 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
                 const uint64_t pbase = (uint64_t)(uint32_t)phys * page_bytes;
 #pragma unroll
                 for (int j = 0; j < BPW; ++j) {
-                    const int lrow = 16 * w + j * RPB;
-                    dma16_s(kb + pbase, dma_off[j], &sm.k[buf][lrow * KPAD]);
-                    dma16_s(vb + pbase, dma_off[j], &sm.v[buf][lrow * KPAD]);
+                    dma16_s(kb + pbase, dma_off[j], lds_k[buf][j]);
+                    dma16_s(vb + pbase, dma_off[j], lds_v[buf][j]);
                 }
             }
         }
