@@ -301,6 +301,20 @@ __device__ inline void dma16_s(const void* sbase, uint32_t voff, uint32_t la) {
                  : "memory", "m0");
 }
 
+// Instruction order of the S^T = K Q^T cluster (KS k-steps of 4 K operand
+// reads and 8 MFMAs): the reads of k-steps 0 and 1, then each k-step's MFMAs
+// followed by the reads of the k-step after next, so that one k-step's LDS
+// reads are always in flight behind the MFMAs.
+template <int KS, int I = 0>
+__device__ inline void qk_schedule() {
+    if constexpr (I == 0) __builtin_amdgcn_sched_group_barrier(0x100, KS > 1 ? 8 : 4, 0);   // DS reads
+    if constexpr (I < KS) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);                                 // MFMAs
+        if constexpr (I + 2 < KS) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        qk_schedule<KS, I + 1>();
+    }
+}
+
 // K and V tiles are row-major (key rows of D halves, KPAD apart); V's O^T
 // operand is read with transposing LDS reads.  DMA: the tiles are written by
 // direct-to-LDS loads in 1 KB blocks, so rows are unpadded and their 16-byte
@@ -561,22 +575,32 @@ void prefill_mfma_kernel(MfmaPrefillArgs a) {
         LLKV_PF_PRIO(D >= 128, 1);
 
         // ---- S^T = K Q^T over the 64 keys: 4 key tiles x 2 query tiles ----
+        // k-step outer: the 8 (key tile, query tile) chains advance together,
+        // and the K operands of k-step ks + 1 are read while those of ks feed
+        // the matrix core.
         f32x4 s[4][2];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
+        auto k_operand = [&](int kt, int ks) {
             // A row c16 of key tile kt = 2*ss + h holds key 32*ss + 8*(c16/4) + 4*h + c16%4
-            const int ss = kt >> 1, h = kt & 1;
-            const int krow = 32 * ss + 8 * (c16 >> 2) + 4 * h + (c16 & 3);
+            const int krow = 32 * (kt >> 1) + 8 * (c16 >> 2) + 4 * (kt & 1) + (c16 & 3);
+            return *reinterpret_cast<const uint4*>(&sm.k[buf][krow * KPAD + scol(krow, ks * 32 + g * 8)]);
+        };
+        uint4 ka[2][4];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) s[kt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kt = 0; kt < 4; ++kt) ka[0][kt] = k_operand(kt, 0);
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const uint4 ka =
-                    *reinterpret_cast<const uint4*>(&sm.k[buf][krow * KPAD + scol(krow, ks * 32 + g * 8)]);
+        for (int ks = 0; ks < KS; ++ks) {
+            if (ks + 1 < KS) {
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) s[kt][nt] = Mfma<T>::mma(ka, qop[nt][ks], s[kt][nt]);
+                for (int kt = 0; kt < 4; ++kt) ka[(ks + 1) & 1][kt] = k_operand(kt, ks + 1);
             }
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    s[kt][nt] = Mfma<T>::mma(ka[ks & 1][kt], qop[nt][ks],
+                                             ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[kt][nt]);
         }
+        if constexpr (kDma) qk_schedule<KS>();
 
         LLKV_PF_PRIO(D >= 128, 0);
         // ---- mask, online softmax (per query column) ----------------------
