@@ -972,6 +972,40 @@ def test_random_shapes(seed):
     _check(out, oracle_prefill(pc, kp, vp), dtype, f"random prefill {seed}", op="prefill")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_layouts(seed):
+    """Seeded shapes over the head layouts the two tests above leave out: decode at head_dim 96
+    and group sizes 12 / 16, prefill at head_dim 96 and 256 (register-staged MFMA kernels) and
+    group sizes up to 16, with fixed, one and automatic splits, causal and not, all three pool
+    types."""
+    rng = np.random.default_rng(7000 + seed)
+    dtype = [torch.float32, torch.float16, torch.bfloat16][seed % 3]
+    d = [64, 96, 128, 256][seed % 4]   # with dtype = seed % 3: every (head_dim, dtype) pair once
+    g = int(rng.choice([1, 2, 4, 8, 12, 16] if d in (64, 128) else [1, 2, 4, 8]))
+    hkv = int(rng.choice([1, 2]))
+    B = int(rng.integers(1, 40))
+    lengths = [int(x) for x in rng.integers(0, int(rng.choice([64, 600, 2500])), B)]
+    S = int(rng.choice([0, 0, 1, 5]))
+    say(f"random layout {seed}: decode {dtype} D={d} G={g} Hkv={hkv} B={B} S={S}")
+    need = sum((L + 1 + 15) // 16 for L in lengths)
+    case = wl.decode_case(f"lay{seed}", B, g * hkv, hkv, d, lengths, need + 8, dtype, seed=seed)
+    out, kp, vp = run_decode(case, num_splits=S)
+    _check(out, oracle_decode(case, np_pool(kp), np_pool(vp), threads=16), dtype, f"layout decode {seed}")
+
+    d = [96, 256, 64, 128][seed // 3]   # each head_dim with all three dtypes
+    g = int(rng.choice([1, 2, 4, 7, 8, 16] if d != 256 else [1, 2, 4]))
+    n = int(rng.integers(1, 5))
+    prefixes = [int(x) for x in rng.integers(0, 1500, n)]
+    chunks = [int(x) for x in rng.integers(1, 300, n)]
+    causal = seed % 4 != 3
+    say(f"random layout {seed}: prefill {dtype} D={d} G={g} Hkv=1 prefixes={prefixes} chunks={chunks} "
+        f"causal={causal}")
+    nb = sum((p_ + c_ + 15) // 16 for p_, c_ in zip(prefixes, chunks)) + 4
+    pc = wl.prefill_case(f"layp{seed}", g, 1, d, prefixes, chunks, {}, nb, dtype, seed=seed, causal=causal)
+    out, kp, vp = run_prefill(pc)
+    _check(out, oracle_prefill(pc, kp, vp), dtype, f"layout prefill {seed}", op="prefill")
+
+
 # 37 and 79: ragged fp16 batches over 4k-key prefixes whose merged chunks went past the bound
 # while key-chunk partials were rounded to fp16; 36 and 276: fp32 head_dim 128 decode at 0.94 and
 # 1.007 of the bound while the score was one and two running sums
